@@ -1,0 +1,224 @@
+"""Benchmark: block-causal attention TFLOP/s (unmasked FLOPs) on one MI355X.
+
+One step = one denoising step's attention at the two headline shapes:
+32 layers of the 1024px text-to-image prefill shape (B1 H24 D128, 256 causal
+text + 4096 image tokens, fresh K/V, ragged L, independent inputs per layer)
+followed by 32 layers of the 768px single-reference edit decode shape (4096
+target queries against a 2560-token slab prefix with bf16 K and fp8e4m3fn V
+plus 4096 fresh keys, uniform L).  Inputs are resident in HBM before timing.
+
+value = unmasked FLOPs of the step / wall time of the step, where a FLOP pair
+counts 2*D for QK^T and 2*D for PV per allowed (query, key) pair.
+
+Prints ONE JSON line (rank 0, N=1).  ``--gpus N`` with N > 1 exits with a
+message: this build runs on one GPU.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "block-causal attn TFLOP/s (unmasked) & % bf16 MFMA peak, 1024px + edit"
+PEAK_BF16_TFLOPS = 2516.6   # MI355X dense bf16 MFMA: 256 CU x 4096 FLOP/clk x 2.4 GHz ("2.5 PF")
+PEAK_HBM_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--layers", type=int, default=32, help="layers per shape in one step")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="target duration of the CPU baseline sample (0 disables it)")
+    ap.add_argument("--only", choices=["t2i_1024", "edit_768"], default=None,
+                    help="time one shape only (profiling aid; the default times both)")
+    return ap.parse_args()
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(wls, budget_s: float) -> dict:
+    """Torch explicit-mask SDPA in fp32 on the host cores, on whole layers of both shapes."""
+    import torch
+
+    from oracle import attention as oa
+
+    threads = torch.get_num_threads()
+    done_flops = 0
+    elapsed = 0.0
+    layers = {"t2i_1024": 0, "edit_768": 0}
+    rep = 0
+    while rep < 3 and (rep == 0 or elapsed < budget_s):
+        for name in ("t2i_1024", "edit_768"):
+            wl = wls.workload(name)
+            inp = wls.make_inputs(wl, seed=9000 + rep, device="cpu")
+            bl = oa.CpuSdpaBaseline(inp["query"], inp["key"], inp["value"], wl.lengths(),
+                                    inp["cache_k"], inp["cache_v"], inp["cache_v_scale"])
+            t0 = time.perf_counter()
+            for b in range(wl.B):
+                for h in range(wl.H):
+                    bl.run(b, h)
+            elapsed += time.perf_counter() - t0
+            done_flops += 4 * wl.D * bl.pairs * wl.B * wl.H
+            layers[name] += 1
+        rep += 1
+    return {
+        "value": round(done_flops / elapsed / 1e12, 6),
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"{layers['t2i_1024']} full layer(s) of t2i_1024 + {layers['edit_768']} of edit_768 "
+                   f"(all 24 heads, fp32 F.scaled_dot_product_attention with a bool [SQ,KV] mask, fp8 V "
+                   f"dequantised first) in {elapsed:.2f} s; torch threads {threads}, os.cpu_count() "
+                   f"{os.cpu_count()}, {cpu_model()}"),
+        "seconds": round(elapsed, 3),
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(per-head work shards without communication, but no multi-GPU path is built)",
+              file=sys.stderr, flush=True)
+        sys.exit(2)
+
+    import torch
+
+    import qwen_image_kernel_amd as qik
+    import qwen_image_kernel_amd.workloads as wls
+
+    assert torch.cuda.is_available(), "bench.py needs a HIP device"
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    names = [args.only] if args.only else ["t2i_1024", "edit_768"]
+
+    # ---- inputs resident in HBM, one independent set per layer
+    layers = {}
+    for name in names:
+        wl = wls.workload(name)
+        layers[name] = [wls.make_inputs(wl, seed=1000 * (wls.NAMES.index(name) + 1) + i, device=dev,
+                                        gen_device="cuda") for i in range(args.layers)]
+    torch.cuda.synchronize()
+
+    calls = []  # (name, fn)
+    for name in names:
+        wl = wls.workload(name)
+        for inp in layers[name]:
+            def fn(wl=wl, inp=inp):
+                return qik.block_causal_flash_attention(
+                    inp["query"], inp["key"], inp["value"], inp["prefix_lengths"], None,
+                    cache_k=inp["cache_k"], cache_v=inp["cache_v"], cache_v_scale=inp["cache_v_scale"],
+                    uniform_full=wl.uniform)
+            calls.append((name, fn))
+    step_flops = sum(wls.workload(n).flops() for n, _ in calls)
+
+    for _ in range(args.warmup):
+        for _, fn in calls:
+            fn()
+    torch.cuda.synchronize()
+
+    # per-launch events on the stream the kernel runs on (torch's current stream)
+    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in calls]
+          for _ in range(args.steps)]
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    t_start.record()
+    for step in range(args.steps):
+        for (name, fn), (e0, e1) in zip(calls, ev[step]):
+            e0.record()
+            fn()
+            e1.record()
+    t_end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    total_ms = t_start.elapsed_time(t_end)
+    per_kernel_ms = {n: [] for n in names}
+    for step in range(args.steps):
+        for (name, _), (e0, e1) in zip(calls, ev[step]):
+            per_kernel_ms[name].append(e0.elapsed_time(e1))
+    ms_per_step = total_ms / args.steps
+    value = step_flops / (ms_per_step * 1e-3) / 1e12
+
+    per_workload = {}
+    for name in names:
+        wl = wls.workload(name)
+        ts = sorted(per_kernel_ms[name])
+        avg = sum(ts) / len(ts)
+        per_workload[name] = {
+            "tflops": round(wl.flops() / (avg * 1e-3) / 1e12, 2),
+            "pct_bf16_peak": round(100 * wl.flops() / (avg * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2),
+            "kernel_avg_us": round(avg * 1e3, 2),
+            "kernel_median_us": round(ts[len(ts) // 2] * 1e3, 2),
+            "launches": len(ts),
+            "unmasked_gflop_per_layer": round(wl.flops() / 1e9, 3),
+            "min_hbm_mb_per_layer": round(wl.min_bytes() / 1e6, 2),
+            "min_hbm_gbs": round(wl.min_bytes() / (avg * 1e-3) / 1e9, 1),
+        }
+    dom = max(names, key=lambda n: per_workload[n]["kernel_avg_us"] * per_workload[n]["launches"])
+    dwl = wls.workload(dom)
+    achieved = dwl.flops() / (per_workload[dom]["kernel_avg_us"] * 1e-6) / 1e12
+
+    cpu = None
+    if args.cpu_seconds > 0:
+        cpu = cpu_baseline(wls, args.cpu_seconds)
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: N(0,1) fp32 cast to bf16, slab V quantised to fp8e4m3fn per (b,h) (amax/448)",
+        "config": {
+            "workload": (f"{args.layers} layers x " + " + ".join(names) + " (D=128, H=24, B=1)"),
+            "t2i_1024": "SQ=SN=4352 (text 256 causal + image 4096 block), fresh K/V, ragged L",
+            "edit_768": "SQ=4096 target, slab P=2560 (bf16 K, fp8 V, capacity P+272) + fresh SN=4096, uniform L",
+            "layers_per_shape": args.layers,
+        },
+        "pct_bf16_peak": round(100 * value / PEAK_BF16_TFLOPS, 2),
+        "roofline": {
+            "bound": "mfma",
+            "kernel": f"attn_fwd_kernel ({dom})",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+            "traffic": None,
+        },
+        "per_workload": per_workload,
+        "cpu_baseline": cpu,
+        "wall_s_timed": round(wall, 3),
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

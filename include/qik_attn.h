@@ -1,0 +1,132 @@
+/*
+ * qik_attn.h -- C ABI of the MI355X (gfx950) block-causal flash attention for
+ * Qwen-Image 2.1, and of the small device helpers that sit beside it.
+ *
+ * Every entry point is plain C: pointers, sizes and strides, no C++ types, no
+ * exceptions across the boundary, no allocation.  Device pointers must point
+ * to memory of the current HIP device; `stream` is a hipStream_t passed as
+ * void* (NULL = the legacy default stream).  All launches are asynchronous
+ * and stream-ordered, like the Triton launch they replace.
+ *
+ * Return value: QIK_OK (0) or a negative qik_status; qik_strerror() names it.
+ */
+#ifndef QIK_ATTN_H
+#define QIK_ATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QIK_ABI_VERSION 1
+
+/* Element types of q / k / v / out. */
+enum qik_dtype {
+  QIK_DTYPE_BF16 = 0,
+  QIK_DTYPE_FP16 = 1
+};
+
+/* Constexpr specialisations of the reference kernel
+ * (qwen_image_kernel/triton_attention.py:57-60), here runtime flags. */
+enum qik_flags {
+  QIK_HAS_CACHE = 1,      /* keys/values = virtual concat [slab prefix (P), fresh (SN)] */
+  QIK_HAS_KEY_VALID = 2,  /* key_valid[b, kv] != 0 gates every key                  */
+  QIK_UNIFORM_L = 4,      /* every row attends [0, P+SN); prefix_lengths not read    */
+  QIK_V_CACHE_FP8 = 8     /* slab V is fp8e4m3fn with a per-(b,h) fp32 scale         */
+};
+
+enum qik_status {
+  QIK_OK = 0,
+  QIK_ERR_NULL_ARG = -1,      /* a required pointer is NULL                          */
+  QIK_ERR_ABI_VERSION = -2,   /* args->abi_version != QIK_ABI_VERSION                */
+  QIK_ERR_DTYPE = -3,         /* q/k/v dtype not bf16/fp16 (triton_attention.py:190) */
+  QIK_ERR_HEAD_DIM = -4,      /* D not in {64, 128}                                  */
+  QIK_ERR_SHAPE = -5,         /* negative or oversized B/SQ/SN/P/H                   */
+  QIK_ERR_CACHE = -6,         /* cache flag / P / pointers inconsistent (:192-196)   */
+  QIK_ERR_FP8_SCALE = -7,     /* fp8 V without scale, without cache, or non-bf16 (:213-216, :159) */
+  QIK_ERR_ALIGN = -8,         /* a pointer or stride breaks the 16-byte row-chunk alignment */
+  QIK_ERR_LAUNCH = -9,        /* the HIP launch failed                               */
+  QIK_ERR_SEGMENTS = -10,     /* bad segment list for the causal-length builder      */
+  QIK_ERR_DEVICE = -11        /* no usable HIP device / device query failed          */
+};
+
+/* Arguments of one attention call.  Layouts are [B, S, H, D] with the D
+ * stride equal to 1; the b/s/h strides below are in ELEMENTS of the tensor
+ * they describe.  This is the argument list of `_qwen21_attn_fwd`
+ * (triton_attention.py:36-63) with the constexprs folded into `flags`. */
+typedef struct qik_attn_args {
+  int32_t abi_version;        /* QIK_ABI_VERSION                                     */
+  int32_t dtype;              /* enum qik_dtype: q, k_new, v_new, k_cache, out       */
+  int32_t flags;              /* enum qik_flags                                      */
+  int32_t reserved0;          /* must be 0                                           */
+
+  const void* q;              /* [B, SQ, H, D]                                       */
+  const void* k_new;          /* [B, SN, H, D]  fresh keys                           */
+  const void* v_new;          /* [B, SN, H, D]  fresh values                         */
+  const void* k_cache;        /* [B, P, H, D]   slab prefix keys (NULL if no cache)  */
+  const void* v_cache;        /* [B, P, H, D]   slab prefix values, dtype or fp8     */
+  const float* v_scale;       /* [B*H] fp32, index b*H+h (only with QIK_V_CACHE_FP8) */
+  const int32_t* prefix_lengths; /* [SQ] int32; row q attends kv <= L[q]; -1 = none */
+  const uint8_t* key_valid;   /* [B, P+SN] bytes, row stride stride_valid_b         */
+  void* out;                  /* [B, SQ, H, D], fully written (zeros for empty rows) */
+  int32_t* debug_tiles;       /* optional [B*H*cdiv(SQ,BM)]: KV tiles visited per row block */
+
+  int64_t B, SQ, SN, P, H, D;
+  int64_t stride_q[3];        /* b, s, h */
+  int64_t stride_k_new[3];
+  int64_t stride_v_new[3];
+  int64_t stride_k_cache[3];
+  int64_t stride_v_cache[3];
+  int64_t stride_out[3];
+  int64_t stride_valid_b;
+  float sm_scale;             /* D**-0.5 in the reference (triton_attention.py:240)  */
+  int32_t reserved1;          /* must be 0                                           */
+} qik_attn_args;
+
+/* ABI version compiled into the library. */
+int qik_abi_version(void);
+
+/* Static text for a status code. */
+const char* qik_strerror(int status);
+
+/* Row-block / KV-tile geometry of the kernel (BM query rows per workgroup,
+ * BN keys per tile).  Replaces the tile table of triton_attention.py:227-232. */
+int qik_attn_block_shape(int32_t* block_m, int32_t* block_n);
+
+/* Host-only argument check: the asserts of block_causal_flash_attention
+ * (triton_attention.py:190-216) plus this kernel's layout limits.  Touches no
+ * device and dereferences no tensor pointer. */
+int qik_attn_validate(const qik_attn_args* args);
+
+/* Block-causal flash attention forward.  Replaces the Triton launch
+ * `_qwen21_attn_fwd[grid](...)` of block_causal_flash_attention
+ * (triton_attention.py:234-259): validates, then enqueues one kernel on
+ * `stream`. */
+int qik_attn_fwd(const qik_attn_args* args, void* stream);
+
+/* Host mirror of the KV-tile schedule the kernel runs: for each row block m
+ * of BM rows, the number of KV tiles visited, summed over the slab and fresh
+ * segments.  A tile of a segment is visited iff its first absolute key index
+ * is <= L_max(m) (the largest L over the block's live rows, or P+SN-1 when
+ * uniform); tiles are segment-local as in triton_attention.py:97-124.
+ * `prefix_lengths` is a HOST array [SQ] (ignored when QIK_UNIFORM_L is set);
+ * `out` is a host array of cdiv(SQ, BM) entries. */
+int qik_attn_tile_schedule(int64_t SQ, int64_t P, int64_t SN, int32_t flags,
+                           const int32_t* prefix_lengths, int32_t* out);
+
+/* Per-row causal-length array on the device, in one launch.  Replaces
+ * _build_prefix_lengths (processors.py:22-36): L = arange(seq_len); for every
+ * non-text segment (start, end), in order: L[q] = end - 1 for the rows q in
+ * [start, end) that exist (end may exceed seq_len, as a slice may); then
+ * L[prefix_end:] = seq_len - 1.  `segments` is a HOST array of nseg triples
+ * (start, end, is_text) with 0 <= start <= end (callers resolve negative
+ * Python indices first); 0 <= prefix_end <= seq_len. */
+int qik_build_prefix_lengths(const int32_t* segments, int32_t nseg, int64_t prefix_end,
+                             int64_t seq_len, int32_t* L, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QIK_ATTN_H */

@@ -1,0 +1,145 @@
+"""ctypes binding of the C ABI declared in include/qik_attn.h.
+
+The shared library is built in-tree (``lib/libqik_attn.so`` next to this file)
+by ``build.py``.  There is no fallback: if the library is missing or fails to
+load, every entry point raises.
+
+torch is imported before the library is opened on purpose.  torch ships its own
+HIP runtime (soname ``libamdhip64.so.7``); loading torch first makes the
+dynamic linker bind this library to that same runtime instance, so the
+``hipStream_t`` handles torch hands out are valid here.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch  # noqa: F401  (load order: torch's HIP runtime first)
+
+LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib")
+LIB_PATH = os.path.join(LIB_DIR, "libqik_attn.so")
+
+ABI_VERSION = 1
+
+DTYPE_BF16 = 0
+DTYPE_FP16 = 1
+
+HAS_CACHE = 1
+HAS_KEY_VALID = 2
+UNIFORM_L = 4
+V_CACHE_FP8 = 8
+
+STATUS_NAMES = {
+    0: "QIK_OK",
+    -1: "QIK_ERR_NULL_ARG",
+    -2: "QIK_ERR_ABI_VERSION",
+    -3: "QIK_ERR_DTYPE",
+    -4: "QIK_ERR_HEAD_DIM",
+    -5: "QIK_ERR_SHAPE",
+    -6: "QIK_ERR_CACHE",
+    -7: "QIK_ERR_FP8_SCALE",
+    -8: "QIK_ERR_ALIGN",
+    -9: "QIK_ERR_LAUNCH",
+    -10: "QIK_ERR_SEGMENTS",
+    -11: "QIK_ERR_DEVICE",
+}
+
+_i64x3 = ctypes.c_int64 * 3
+
+
+class QikAttnArgs(ctypes.Structure):
+    """Mirror of ``struct qik_attn_args`` (include/qik_attn.h)."""
+
+    _fields_ = [
+        ("abi_version", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("flags", ctypes.c_int32),
+        ("reserved0", ctypes.c_int32),
+        ("q", ctypes.c_void_p),
+        ("k_new", ctypes.c_void_p),
+        ("v_new", ctypes.c_void_p),
+        ("k_cache", ctypes.c_void_p),
+        ("v_cache", ctypes.c_void_p),
+        ("v_scale", ctypes.c_void_p),
+        ("prefix_lengths", ctypes.c_void_p),
+        ("key_valid", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("debug_tiles", ctypes.c_void_p),
+        ("B", ctypes.c_int64),
+        ("SQ", ctypes.c_int64),
+        ("SN", ctypes.c_int64),
+        ("P", ctypes.c_int64),
+        ("H", ctypes.c_int64),
+        ("D", ctypes.c_int64),
+        ("stride_q", _i64x3),
+        ("stride_k_new", _i64x3),
+        ("stride_v_new", _i64x3),
+        ("stride_k_cache", _i64x3),
+        ("stride_v_cache", _i64x3),
+        ("stride_out", _i64x3),
+        ("stride_valid_b", ctypes.c_int64),
+        ("sm_scale", ctypes.c_float),
+        ("reserved1", ctypes.c_int32),
+    ]
+
+
+# (name, restype, argtypes) of every exported entry point
+EXPORTS = (
+    ("qik_abi_version", ctypes.c_int, ()),
+    ("qik_strerror", ctypes.c_char_p, (ctypes.c_int,)),
+    ("qik_attn_block_shape", ctypes.c_int, (ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32))),
+    ("qik_attn_validate", ctypes.c_int, (ctypes.POINTER(QikAttnArgs),)),
+    ("qik_attn_fwd", ctypes.c_int, (ctypes.POINTER(QikAttnArgs), ctypes.c_void_p)),
+    (
+        "qik_attn_tile_schedule",
+        ctypes.c_int,
+        (ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p),
+    ),
+    (
+        "qik_build_prefix_lengths",
+        ctypes.c_int,
+        (ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p),
+    ),
+)
+
+_lock = threading.Lock()
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Open the in-tree library once; raise if it is absent or incompatible."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"qwen_image_kernel_amd: HIP library not built ({LIB_PATH} missing); "
+                "run __graft_entry__.build() or python -m qwen_image_kernel_amd.build"
+            )
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, restype, argtypes in EXPORTS:
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = list(argtypes)
+        ver = lib.qik_abi_version()
+        if ver != ABI_VERSION:
+            raise RuntimeError(f"qwen_image_kernel_amd: library ABI {ver} != binding ABI {ABI_VERSION}")
+        _lib = lib
+    return _lib
+
+
+def strerror(status: int) -> str:
+    msg = load().qik_strerror(int(status))
+    return msg.decode() if msg else "unknown"
+
+
+def check(status: int, what: str) -> None:
+    """Raise RuntimeError for a nonzero status (the reference raises on launch errors)."""
+    if status != 0:
+        name = STATUS_NAMES.get(int(status), str(status))
+        raise RuntimeError(f"{what} failed: {name}: {strerror(status)}")

@@ -1,0 +1,267 @@
+"""Block-causal flash attention entry point, same signature as the reference.
+
+``block_causal_flash_attention`` keeps the argument list, defaults, asserts and
+output allocation of ``qwen_image_kernel/triton_attention.py:171-260`` and hands
+the call to the gfx950 HIP kernel through the C ABI (``qik_attn_fwd``).  The
+launch is asynchronous on the current stream of the query's device, like the
+Triton launch it replaces.
+
+Also here: ``build_prefix_lengths`` (the per-row causal-length array of
+``processors.py:22-36``, built on the device in one launch) and
+``tile_schedule`` (the host mirror of the kernel's KV-tile schedule).
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import torch
+
+from . import _lib
+
+__all__ = [
+    "block_causal_flash_attention",
+    "build_prefix_lengths",
+    "tile_schedule",
+    "block_shape",
+    "make_args",
+]
+
+_DTYPES = {torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_FP16}
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _bsh(t: torch.Tensor) -> tuple[int, int, int]:
+    return (t.stride(0), t.stride(1), t.stride(2))
+
+
+def _check_rows(name: str, t: torch.Tensor) -> None:
+    if t.dim() != 4:
+        raise ValueError(f"{name} must be [B, S, H, D], got shape {tuple(t.shape)}")
+    if t.shape[-1] > 1 and t.stride(-1) != 1:
+        raise ValueError(f"{name} must have unit stride along D (got stride {t.stride(-1)})")
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor (the kernel runs on the GPU)")
+
+
+def make_args(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    prefix_lengths: torch.Tensor | None,
+    kv_bytes: torch.Tensor | None,
+    out: torch.Tensor,
+    cache_k: torch.Tensor | None,
+    cache_v: torch.Tensor | None,
+    cache_v_scale: torch.Tensor | None,
+    uniform: bool,
+    debug_tiles: torch.Tensor | None = None,
+) -> _lib.QikAttnArgs:
+    """Fill the C argument struct from tensors (no device work)."""
+    B, SQ, H, D = query.shape
+    P = 0 if cache_k is None else cache_k.shape[1]
+    a = _lib.QikAttnArgs()
+    a.abi_version = _lib.ABI_VERSION
+    a.dtype = _DTYPES[query.dtype]
+    flags = 0
+    if P > 0:
+        flags |= _lib.HAS_CACHE
+    if kv_bytes is not None:
+        flags |= _lib.HAS_KEY_VALID
+    if uniform:
+        flags |= _lib.UNIFORM_L
+    if cache_v_scale is not None:
+        flags |= _lib.V_CACHE_FP8
+    a.flags = flags
+    a.q = _ptr(query)
+    a.k_new = _ptr(key)
+    a.v_new = _ptr(value)
+    a.out = _ptr(out)
+    a.prefix_lengths = _ptr(prefix_lengths)
+    a.key_valid = _ptr(kv_bytes)
+    a.debug_tiles = _ptr(debug_tiles)
+    a.B, a.SQ, a.SN, a.P, a.H, a.D = B, SQ, key.shape[1], P, H, D
+    a.stride_q = _lib._i64x3(*_bsh(query))
+    a.stride_k_new = _lib._i64x3(*_bsh(key))
+    a.stride_v_new = _lib._i64x3(*_bsh(value))
+    a.stride_out = _lib._i64x3(*_bsh(out))
+    if P > 0:
+        a.k_cache = _ptr(cache_k)
+        a.v_cache = _ptr(cache_v)
+        a.stride_k_cache = _lib._i64x3(*_bsh(cache_k))
+        a.stride_v_cache = _lib._i64x3(*_bsh(cache_v))
+        a.v_scale = _ptr(cache_v_scale)
+    a.stride_valid_b = kv_bytes.stride(0) if kv_bytes is not None else 0
+    # fp32 D**-0.5, as the Triton launch passes query.shape[-1] ** -0.5 (triton_attention.py:240)
+    a.sm_scale = float(D) ** -0.5
+    return a
+
+
+def block_causal_flash_attention(
+    query: torch.Tensor,  # [B, SQ, H, D]
+    key: torch.Tensor,  # [B, SN, H, D]  fresh keys
+    value: torch.Tensor,  # [B, SN, H, D]
+    prefix_lengths: torch.Tensor,  # [SQ] int32
+    key_valid: torch.Tensor | None,  # [B, KV_TOTAL] bool or None
+    cache_k: torch.Tensor | None = None,  # [B, P, H, D]
+    cache_v: torch.Tensor | None = None,
+    cache_v_scale: torch.Tensor | None = None,  # [B, H] fp32, only with fp8 cache V
+    uniform_full: bool = False,  # caller guarantee: L == KV_TOTAL-1 for every row
+    *,
+    debug_tiles: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Exact block-causal attention via per-row prefix lengths.
+
+    Row q attends key kv iff kv <= prefix_lengths[q] (and key_valid[b, kv] when
+    given).  With ``cache_k``/``cache_v`` the keys/values are the virtual
+    concatenation [cache, key] and ``prefix_lengths``/``key_valid`` index that
+    absolute space; nothing is concatenated.  Rows with L = -1 produce zeros.
+    With ``cache_v_scale`` the cache V is fp8e4m3fn dequantised per (b, h) as
+    bf16(fp32(v) * scale).  Semantics: triton_attention.py:171-260.
+
+    ``debug_tiles`` (keyword only, not in the reference) receives the number of
+    KV tiles visited per (b, h, row block), int32 [B*H*cdiv(SQ, BM)].
+    """
+    assert query.dtype in (torch.bfloat16, torch.float16), "fp16/bf16 only"
+    B, SQ, H, D = query.shape
+    if cache_k is not None:
+        P = cache_k.shape[1]
+        SN = key.shape[1]
+        assert cache_k.shape[2] == H and key.shape[2] == H
+        assert cache_k.dtype == key.dtype
+    else:
+        P = 0
+        SN = key.shape[1]
+    KV_TOTAL = P + SN
+    assert key.dtype == query.dtype and value.dtype == query.dtype, "q/k/v dtypes must match"
+    for name, t in (("query", query), ("key", key), ("value", value)):
+        _check_rows(name, t)
+    if P > 0:
+        assert cache_v is not None and cache_v.shape[:3] == cache_k.shape[:3]
+        _check_rows("cache_k", cache_k)
+        _check_rows("cache_v", cache_v)
+
+    out = torch.empty_like(query)
+    if out.stride(-1) != 1:
+        out = torch.empty(query.shape, dtype=query.dtype, device=query.device)
+
+    kv_bytes = None
+    if key_valid is not None:
+        kv_bytes = key_valid.to(torch.uint8).contiguous()
+        assert kv_bytes.dim() == 2 and kv_bytes.shape[1] >= KV_TOTAL, "key_valid must be [B, KV_TOTAL]"
+        if kv_bytes.shape[0] == 1 and B > 1:
+            kv_bytes = kv_bytes.expand(B, -1)
+
+    v_fp8 = cache_v_scale is not None
+    scale = None
+    if v_fp8:
+        assert cache_v is not None and cache_v.dtype == torch.float8_e4m3fn
+        scale = cache_v_scale
+        if scale.dtype != torch.float32 or not scale.is_contiguous():
+            scale = scale.float().contiguous()
+        assert scale.numel() == B * H, "cache_v_scale must be [B, H]"
+    elif P > 0:
+        assert cache_v.dtype == query.dtype, "bf16/fp16 cache V must match the query dtype"
+
+    uniform = uniform_full and key_valid is None
+
+    L = None
+    if not uniform:
+        L = prefix_lengths
+        if L.dtype != torch.int32 or not L.is_contiguous():
+            L = L.to(torch.int32).contiguous()
+        assert L.numel() >= SQ, "prefix_lengths must be [SQ]"
+
+    # with P == 0 the slab (and its fp8 scale) is never read (HAS_CACHE = P > 0, :250)
+    args = make_args(query, key, value, L, kv_bytes, out, cache_k if P > 0 else None,
+                     cache_v if P > 0 else None, scale if P > 0 else None, uniform, debug_tiles)
+    lib = _lib.load()
+    dev = query.device
+    if dev.index is not None and dev.index != torch.cuda.current_device():
+        with torch.cuda.device(dev):
+            stream = torch.cuda.current_stream(dev).cuda_stream
+            st = lib.qik_attn_fwd(ctypes.byref(args), ctypes.c_void_p(stream))
+    else:
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        st = lib.qik_attn_fwd(ctypes.byref(args), ctypes.c_void_p(stream))
+    _lib.check(st, "qik_attn_fwd")
+    return out
+
+
+def _norm_slice(start: int, stop: int | None, n: int) -> tuple[int, int]:
+    s, e, _ = slice(start, stop).indices(n)
+    return s, max(s, e)
+
+
+def build_prefix_lengths(
+    segments: list[tuple[int, int, bool]], prefix_len: int, seq_len: int, device: torch.device
+) -> torch.Tensor:
+    """Per-row inclusive kv limit L: row q attends iff kv <= L[q] (processors.py:22-36).
+
+    text run (s, e)      -> L[s:e] = s..e-1  (causal)
+    image run (s, e)     -> L[s:e] = e-1     (bidirectional block + full prefix)
+    target rows [P, S)   -> L = S-1          (full attention)
+
+    The fill value of an image run is ``end - 1`` even when ``end`` exceeds
+    ``seq_len``, and ``prefix_len`` follows Python slice semantics, as the
+    reference's slice assignments do.  Negative segment bounds raise ValueError
+    (the reference would write negative lengths).  The array is filled on
+    ``device`` by one HIP launch.
+    """
+    device = torch.device(device)
+    if device.type != "cuda":
+        raise ValueError("build_prefix_lengths builds L on the GPU; pass a device tensor's device")
+    L = torch.empty(seq_len, dtype=torch.int32, device=device)
+    rows = []
+    for s, e, is_text in segments:
+        if s < 0 or e < 0:
+            raise ValueError(f"segment ({s}, {e}) has a negative bound")
+        if e > s:  # an empty or reversed slice assigns nothing
+            rows.append((s, e, 1 if is_text else 0))
+    segs = np.zeros((max(len(rows), 1), 3), dtype=np.int32)
+    for i, r in enumerate(rows):
+        segs[i] = r
+    pe, _ = _norm_slice(prefix_len, None, seq_len)
+    lib = _lib.load()
+    with torch.cuda.device(device):
+        stream = torch.cuda.current_stream(device).cuda_stream
+        st = lib.qik_build_prefix_lengths(
+            segs.ctypes.data, len(rows), pe, seq_len, L.data_ptr(), ctypes.c_void_p(stream)
+        )
+    _lib.check(st, "qik_build_prefix_lengths")
+    return L
+
+
+def block_shape() -> tuple[int, int]:
+    """(BM, BN): query rows per workgroup and keys per KV tile of the kernel."""
+    bm, bn = ctypes.c_int32(), ctypes.c_int32()
+    _lib.check(_lib.load().qik_attn_block_shape(ctypes.byref(bm), ctypes.byref(bn)), "qik_attn_block_shape")
+    return bm.value, bn.value
+
+
+def tile_schedule(
+    SQ: int, P: int, SN: int, prefix_lengths: np.ndarray | torch.Tensor | None, uniform: bool
+) -> np.ndarray:
+    """KV tiles the kernel visits per row block (host computation, no device).
+
+    Returns int32 [cdiv(SQ, BM)]; the same numbers the kernel writes into
+    ``debug_tiles`` for every (b, h).
+    """
+    bm, _ = block_shape()
+    flags = (_lib.HAS_CACHE if P > 0 else 0) | (_lib.UNIFORM_L if uniform else 0)
+    Lh = None
+    if not uniform:
+        if isinstance(prefix_lengths, torch.Tensor):
+            prefix_lengths = prefix_lengths.detach().cpu().numpy()
+        Lh = np.ascontiguousarray(prefix_lengths, dtype=np.int32)
+        assert Lh.size >= SQ
+    out = np.zeros(max(-(-SQ // bm), 1), dtype=np.int32)
+    st = _lib.load().qik_attn_tile_schedule(
+        SQ, P, SN, flags, None if Lh is None else Lh.ctypes.data, out.ctypes.data
+    )
+    _lib.check(st, "qik_attn_tile_schedule")
+    return out[: -(-SQ // bm)]

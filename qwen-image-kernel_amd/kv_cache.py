@@ -1,0 +1,102 @@
+"""Contiguous prefix-KV slab, same attributes and layout as the reference.
+
+``ContiguousKVCache`` / ``_LayerView`` keep the API of
+``qwen_image_kernel/kv_cache.py:23-95``: one preallocated slab for all layers,
+K ``[L, B, H, P_max, D]`` in the model dtype, V the same or fp8e4m3fn with one
+fp32 scale per (layer, b, h), and ``lengths [L]`` int64 on the device.  Each
+head's prefix tokens are dense (256 B rows of bf16 K, 128 B rows of fp8 V), and
+``views()`` returns ``[B, P, H, D]`` strided views that the attention kernel
+reads in place.
+
+Difference from the reference: the prefix length of each layer is also kept on
+the host, so ``get()``/``views()`` do not synchronise the device
+(the reference reads ``int(lengths[layer])``, kv_cache.py:49, 56).
+"""
+
+from __future__ import annotations
+
+import torch
+
+FP8_E4M3_MAX = 448.0
+
+
+class _LayerView:
+    """Per-layer store/get interface compatible with the stock cache."""
+
+    def __init__(self, cache: "ContiguousKVCache", layer: int):
+        self._c = cache
+        self._layer = layer
+
+    def store(self, k: torch.Tensor, v: torch.Tensor) -> None:
+        """k, v: [B, P, H, D] post-RoPE; V is quantised per (b, h) when the slab is fp8.
+
+        Quantisation (kv_cache.py:36-42): scale = max(amax|v| / 448, 1e-12) in
+        fp32, code = e4m3fn(clamp(v / scale, +-448)) with a true fp32 division
+        and round-to-nearest-even.
+        """
+        c = self._c
+        P = k.shape[1]
+        if P > c.capacity:
+            raise ValueError(f"prefix of {P} tokens exceeds the slab capacity {c.capacity}")
+        c.k_buf[self._layer, :, :, :P, :].copy_(k.transpose(1, 2))
+        if c.v_fp8:
+            vt = v.transpose(1, 2).float()
+            scale = vt.abs().amax(dim=(2, 3)).float() / FP8_E4M3_MAX
+            scale = scale.clamp_min(1e-12)
+            vq = (vt / scale[:, :, None, None]).clamp(-FP8_E4M3_MAX, FP8_E4M3_MAX).to(torch.float8_e4m3fn)
+            c.v_buf[self._layer, :, :, :P, :].copy_(vq)
+            c.v_scale[self._layer].copy_(scale)
+        else:
+            c.v_buf[self._layer, :, :, :P, :].copy_(v.transpose(1, 2))
+        c.lengths[self._layer] = P
+        c._host_lengths[self._layer] = P
+
+    def get(self):
+        """(k, v) as [B, P, H, D] strided views."""
+        P = self._c._host_lengths[self._layer]
+        k = self._c.k_buf[self._layer, :, :, :P, :].transpose(1, 2)
+        v = self._c.v_buf[self._layer, :, :, :P, :].transpose(1, 2)
+        return k, v
+
+    def views(self):
+        """(k, v, v_scale_or_None) for block_causal_flash_attention."""
+        P = self._c._host_lengths[self._layer]
+        k = self._c.k_buf[self._layer, :, :, :P, :].transpose(1, 2)
+        v = self._c.v_buf[self._layer, :, :, :P, :].transpose(1, 2)
+        scale = self._c.v_scale[self._layer] if self._c.v_fp8 else None
+        return k, v, scale
+
+
+class ContiguousKVCache:
+    """Single-slab prefix KV cache: one allocation per buffer for all layers.
+
+    K layout: [L, B, H, P_max, D] (dtype).  V layout: same (dtype) or fp8e4m3fn
+    with per-head fp32 scales [L, B, H].  Per prefix token across 32 layers at
+    H*D = 3072: K+V bf16 = 384 KB, K bf16 + V fp8 = 288 KB.
+    """
+
+    def __init__(
+        self,
+        num_layers: int,
+        batch: int,
+        prefix_max: int,
+        num_heads: int,
+        head_dim: int,
+        v_fp8: bool = False,
+        device: torch.device | str = "cuda",
+        dtype: torch.dtype = torch.bfloat16,
+    ):
+        self.v_fp8 = v_fp8
+        self.num_layers = num_layers
+        self.capacity = prefix_max
+        self.batch_size = batch
+        self.k_buf = torch.empty(num_layers, batch, num_heads, prefix_max, head_dim, dtype=dtype, device=device)
+        v_dtype = torch.float8_e4m3fn if v_fp8 else dtype
+        self.v_buf = torch.empty(num_layers, batch, num_heads, prefix_max, head_dim, dtype=v_dtype, device=device)
+        self.v_scale = torch.empty(num_layers, batch, num_heads, dtype=torch.float32, device=device)
+        self.lengths = torch.zeros(num_layers, dtype=torch.int64, device=device)
+        self._host_lengths = [0] * num_layers
+        self.layers = [_LayerView(self, i) for i in range(num_layers)]
+
+    def get_layer(self, i: int) -> _LayerView:
+        return self.layers[i]

@@ -1,0 +1,178 @@
+"""C ABI: exports, struct layout, host-side validation and the schedule mirror (CPU only).
+
+No test here launches a kernel: qik_attn_validate and qik_attn_tile_schedule
+are host-only, and qik_attn_fwd is only called with arguments it rejects (or
+with no work) before any device call.
+"""
+
+import ctypes
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+from oracle import schedule as osch
+
+import qwen_image_kernel_amd.workloads as wls
+from qwen_image_kernel_amd import _lib, attention
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "qik_attn.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^[A-Za-z_][\w\s\*]*?\b(qik_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = header_functions()
+    assert len(names) >= 7
+    for n in names:
+        assert hasattr(lib, n), n
+    assert {n for n, _, _ in _lib.EXPORTS} == set(names)
+    assert lib.qik_abi_version() == _lib.ABI_VERSION
+
+
+def test_struct_layout_matches_c_header(tmp_path):
+    fields = [f for f, _ in _lib.QikAttnArgs._fields_]
+    src = ["#include <stdio.h>", "#include <stddef.h>", '#include "qik_attn.h"', "int main(void) {",
+           'printf("sizeof %zu\\n", sizeof(qik_attn_args));']
+    for f in fields:
+        src.append(f'printf("{f} %zu\\n", offsetof(qik_attn_args, {f}));')
+    src.append("return 0; }")
+    c = tmp_path / "layout.c"
+    c.write_text("\n".join(src))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", f"-I{os.path.dirname(HEADER)}", str(c), "-o", str(exe)], check=True)
+    got = dict(line.split() for line in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                        check=True).stdout.splitlines())
+    assert int(got["sizeof"]) == ctypes.sizeof(_lib.QikAttnArgs)
+    for f in fields:
+        assert int(got[f]) == getattr(_lib.QikAttnArgs, f).offset, f
+
+
+def _valid_args(**kw):
+    a = _lib.QikAttnArgs()
+    a.abi_version = _lib.ABI_VERSION
+    a.dtype = _lib.DTYPE_BF16
+    a.flags = 0
+    B, SQ, SN, H, D = 1, 300, 300, 4, 128
+    a.B, a.SQ, a.SN, a.P, a.H, a.D = B, SQ, SN, 0, H, D
+    fake = 0x10000
+    a.q, a.k_new, a.v_new, a.out, a.prefix_lengths = fake, fake, fake, fake, fake
+    st = (SQ * H * D, H * D, D)
+    for f in ("stride_q", "stride_k_new", "stride_v_new", "stride_out"):
+        setattr(a, f, _lib._i64x3(*st))
+    a.sm_scale = D ** -0.5
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+def _validate(a):
+    return _lib.load().qik_attn_validate(ctypes.byref(a))
+
+
+def test_validate_accepts_reference_call_patterns():
+    assert _validate(_valid_args()) == 0
+    # decode: slab views [B, P, H, D] with strides (H*Pmax*D, D, Pmax*D) and fp8 V
+    a = _valid_args(P=256, flags=_lib.HAS_CACHE | _lib.V_CACHE_FP8 | _lib.UNIFORM_L)
+    a.k_cache = a.v_cache = a.v_scale = 0x20000
+    a.stride_k_cache = a.stride_v_cache = _lib._i64x3(4 * 528 * 128, 128, 528 * 128)
+    a.prefix_lengths = None
+    assert _validate(a) == 0
+    # fresh V as a strided view of a fused QKV output: stride_s = 3*H*D
+    a = _valid_args()
+    a.stride_v_new = _lib._i64x3(300 * 3 * 4 * 128, 3 * 4 * 128, 128)
+    assert _validate(a) == 0
+
+
+@pytest.mark.parametrize(
+    "mutate,code",
+    [
+        (lambda a: setattr(a, "abi_version", 99), -2),
+        (lambda a: setattr(a, "reserved0", 1), -2),
+        (lambda a: setattr(a, "dtype", 7), -3),              # triton_attention.py:190
+        (lambda a: setattr(a, "D", 96), -4),
+        (lambda a: setattr(a, "SQ", -1), -5),
+        (lambda a: setattr(a, "flags", 64), -5),
+        (lambda a: setattr(a, "P", 16), -6),                 # P > 0 without HAS_CACHE (:192-196)
+        (lambda a: setattr(a, "flags", _lib.HAS_CACHE), -6),  # HAS_CACHE with P == 0
+        (lambda a: setattr(a, "flags", _lib.V_CACHE_FP8), -7),  # fp8 V without a cache (:213-216)
+        (lambda a: setattr(a, "v_scale", 0x30000), -7),      # a scale without fp8 V
+        (lambda a: setattr(a, "flags", _lib.HAS_KEY_VALID), -1),
+        (lambda a: setattr(a, "q", None), -1),
+        (lambda a: setattr(a, "prefix_lengths", None), -1),
+        (lambda a: setattr(a, "q", 0x10008), -8),
+        (lambda a: setattr(a, "stride_k_new", _lib._i64x3(300 * 512, 516, 128)), -8),
+    ],
+)
+def test_validate_error_codes(mutate, code):
+    a = _valid_args()
+    mutate(a)
+    assert _validate(a) == code
+    # qik_attn_fwd validates first and returns the same code without a device call
+    assert _lib.load().qik_attn_fwd(ctypes.byref(a), None) == code
+    assert _lib.STATUS_NAMES[code] and _lib.strerror(code) != "unknown qik status"
+
+
+def test_fp8_requires_bf16():
+    a = _valid_args(P=64, dtype=_lib.DTYPE_FP16, flags=_lib.HAS_CACHE | _lib.V_CACHE_FP8)
+    a.k_cache = a.v_cache = a.v_scale = 0x20000
+    a.stride_k_cache = a.stride_v_cache = _lib._i64x3(4 * 64 * 128, 128, 64 * 128)
+    assert _validate(a) == -7
+
+
+def test_fwd_without_work_is_a_no_op():
+    a = _valid_args(SQ=0)
+    assert _lib.load().qik_attn_fwd(ctypes.byref(a), None) == 0
+
+
+def test_segment_validation_is_host_side():
+    lib = _lib.load()
+    bad = np.array([[5, 3, 0]], dtype=np.int32)
+    assert lib.qik_build_prefix_lengths(bad.ctypes.data, 1, 0, 10, None, None) == -10
+    neg = np.array([[-1, 3, 0]], dtype=np.int32)
+    assert lib.qik_build_prefix_lengths(neg.ctypes.data, 1, 0, 10, None, None) == -10
+    ok = np.array([[0, 3, 0]], dtype=np.int32)
+    assert lib.qik_build_prefix_lengths(ok.ctypes.data, 1, 11, 10, None, None) == -10   # prefix_end > seq_len
+    assert lib.qik_build_prefix_lengths(ok.ctypes.data, 1, 0, 0, None, None) == 0       # nothing to fill
+
+
+@pytest.mark.parametrize("name", wls.NAMES)
+def test_schedule_mirror_equals_oracle_exact_rule(name):
+    wl = wls.workload(name)
+    bm, bn = attention.block_shape()
+    got = attention.tile_schedule(wl.SQ, wl.P, wl.SN, wl.lengths(), wl.uniform)
+    want = osch.exact_rule(wl.lengths(), wl.SQ, wl.P, wl.SN, bm, bn, wl.P > 0, wl.uniform)
+    np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("seed", range(30))
+def test_schedule_mirror_random(seed):
+    rng = np.random.default_rng(seed)
+    SQ = int(rng.integers(1, 700))
+    P = int(rng.integers(0, 2)) * int(rng.integers(1, 500))
+    SN = int(rng.integers(1, 700))
+    L = rng.integers(-1, P + SN + 3, size=SQ).astype(np.int32)
+    bm, bn = attention.block_shape()
+    for uniform in (False, True):
+        got = attention.tile_schedule(SQ, P, SN, L, uniform)
+        want = osch.exact_rule(L, SQ, P, SN, bm, bn, P > 0, uniform)
+        np.testing.assert_array_equal(got, want)
+
+
+def test_wrapper_keeps_reference_asserts_on_cpu():
+    import torch
+    q = torch.zeros(1, 8, 2, 128)
+    with pytest.raises(AssertionError, match="fp16/bf16 only"):
+        attention.block_causal_flash_attention(q, q, q, torch.zeros(8, dtype=torch.int32), None)
+    qb = q.to(torch.bfloat16)
+    ck = torch.zeros(1, 4, 3, 128, dtype=torch.bfloat16)
+    with pytest.raises(AssertionError):
+        attention.block_causal_flash_attention(qb, qb, qb, torch.zeros(8, dtype=torch.int32), None,
+                                               cache_k=ck, cache_v=ck)

@@ -1,0 +1,89 @@
+"""Oracle: fp8e4m3fn / bf16 rounding and the slab quantisation (CPU)."""
+
+import numpy as np
+import torch
+
+from oracle import fp8 as of
+
+
+def test_decode_table_closed_form_points():
+    t = of.e4m3fn_decode_table()
+    assert t[0x00] == 0.0 and np.signbit(t[0x80])
+    assert t[0x01] == 2.0 ** -9            # smallest subnormal
+    assert t[0x07] == 7 * 2.0 ** -9        # largest subnormal
+    assert t[0x08] == 2.0 ** -6            # smallest normal
+    assert t[0x38] == 1.0                  # exponent 7 = bias
+    assert t[0x7E] == 448.0 and t[0xFE] == -448.0
+    assert np.isnan(t[0x7F]) and np.isnan(t[0xFF])
+    pos = t[:127]
+    assert (np.diff(pos) > 0).all()        # codes 0..126 are increasing
+
+
+def test_decode_table_matches_torch():
+    tt = torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).float().numpy()
+    t = of.e4m3fn_decode_table()
+    same = (t == tt) | (np.isnan(t) & np.isnan(tt))
+    assert same.all()
+
+
+def test_encode_rne_matches_torch_cast():
+    rng = np.random.default_rng(0)
+    x = np.concatenate([
+        (rng.standard_normal(200000) * 40).astype(np.float32),
+        (rng.standard_normal(50000) * 1e-2).astype(np.float32),   # subnormal range
+    ]).clip(-448, 448)
+    t = of.e4m3fn_decode_table()[:127].astype(np.float64)
+    mids = ((t[:-1] + t[1:]) / 2).astype(np.float32)             # exact ties
+    x = np.concatenate([x, mids, -mids, np.float32([0.0, -0.0, 448.0, -448.0, 2.0 ** -10])])
+    want = torch.from_numpy(x).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    np.testing.assert_array_equal(of.e4m3fn_encode(x), want)
+
+
+def test_ties_go_to_even_mantissa():
+    # 1.0 = 0x38, next is 1.125 = 0x39; the midpoint 1.0625 rounds to the even code 0x38
+    assert of.e4m3fn_encode(np.float32([1.0625]))[0] == 0x38
+    # 1.125 = 0x39 and 1.25 = 0x3A; midpoint 1.1875 -> 0x3A (even)
+    assert of.e4m3fn_encode(np.float32([1.1875]))[0] == 0x3A
+    # half the smallest subnormal ties to zero
+    assert of.e4m3fn_encode(np.float32([2.0 ** -10]))[0] == 0x00
+
+
+def test_bf16_round_matches_torch():
+    rng = np.random.default_rng(1)
+    u = rng.integers(0, 2 ** 32, size=200000, dtype=np.uint64).astype(np.uint32)
+    u = u[(u & 0x7F800000) != 0x7F800000]   # finite only
+    x = u.view(np.float32)
+    want = torch.from_numpy(x.copy()).to(torch.bfloat16).float().numpy()
+    np.testing.assert_array_equal(of.bf16_round(x), want)
+
+
+def _torch_store(v):
+    """The slab store's quantisation written with torch library ops on the CPU."""
+    vt = v.transpose(1, 2).float()
+    scale = vt.abs().amax(dim=(2, 3)).float() / 448.0
+    scale = scale.clamp_min(1e-12)
+    vq = (vt / scale[:, :, None, None]).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+    return vq.view(torch.uint8).numpy(), scale.numpy()
+
+
+def test_quantize_per_head_matches_torch_ops():
+    g = torch.Generator().manual_seed(3)
+    v = torch.randn(2, 96, 3, 128, generator=g).to(torch.bfloat16)
+    v[0, :, 1] *= 1e-3                      # a small-magnitude head
+    v[1, :, 2] = 0                          # an all-zero head -> scale clamps to 1e-12
+    codes, scale = of.quantize_per_head(v.float().numpy())
+    tc, ts = _torch_store(v)
+    np.testing.assert_array_equal(scale, ts)
+    np.testing.assert_array_equal(codes, tc)
+    assert scale[1, 2] == np.float32(1e-12)
+
+
+def test_quantize_round_trip_error_bound():
+    """fp8-V store/dequant relative error < 0.03 (tests/test_kv_cache.py:29-38)."""
+    g = torch.Generator().manual_seed(4)
+    v = torch.randn(1, 640, 4, 128, generator=g).to(torch.bfloat16)
+    codes, scale = of.quantize_per_head(v.float().numpy())
+    deq = of.dequant_bf16(codes, scale[:, :, None, None])            # [B, H, P, D]
+    ref = v.float().numpy().transpose(0, 2, 1, 3)
+    rel = np.linalg.norm(deq - ref) / np.linalg.norm(ref)
+    assert rel < 0.03
