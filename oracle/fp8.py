@@ -66,12 +66,17 @@ def quantize_per_head(v: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     """Slab V quantisation of kv_cache.py:36-42 for v [B, P, H, D].
 
     Returns (codes uint8 [B, H, P, D], scale float32 [B, H]) with
-    scale = max(amax|v| / 448, 1e-12) in fp32 and
+    scale = max(amax|v| * fp32(1/448), 1e-12) and
     code = e4m3fn(clamp(v / scale, -448, 448)) using a true fp32 division.
+
+    The reference runs this on the GPU, where torch evaluates ``tensor / 448.0``
+    (a host scalar divisor) as a multiply by the fp32 reciprocal, while
+    ``tensor / tensor`` is a true division; both are restated here.
     """
     vt = np.ascontiguousarray(np.asarray(v, dtype=np.float32).transpose(0, 2, 1, 3))
     amax = np.abs(vt).max(axis=(2, 3)).astype(np.float32)
-    scale = np.maximum(amax / np.float32(E4M3_MAX), np.float32(1e-12)).astype(np.float32)
+    inv = np.float32(1.0) / np.float32(E4M3_MAX)
+    scale = np.maximum(amax * inv, np.float32(1e-12)).astype(np.float32)
     q = np.clip(vt / scale[:, :, None, None], -E4M3_MAX, E4M3_MAX).astype(np.float32)
     return e4m3fn_encode(q), scale
 

@@ -235,7 +235,7 @@ def test_deterministic():
 
 def test_misaligned_input_is_rejected():
     g = torch.Generator().manual_seed(960)
-    base = _rand((1, 64 * 4 * 128 + 4,), g).to(DEV)
+    base = _rand((64 * 4 * 128 + 4,), g).to(DEV)
     q = base[4:].view(1, 64, 4, 128)                 # 8-byte offset: not 16-byte aligned
     L = torch.arange(64, dtype=torch.int32, device=DEV)
     with pytest.raises(RuntimeError, match="QIK_ERR_ALIGN"):

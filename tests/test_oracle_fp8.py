@@ -58,9 +58,13 @@ def test_bf16_round_matches_torch():
 
 
 def _torch_store(v):
-    """The slab store's quantisation written with torch library ops on the CPU."""
+    """The slab store's quantisation written with torch library ops on the CPU.
+
+    ``amax * (1 / 448)`` is how torch on the GPU evaluates the reference's
+    ``amax / 448.0`` (scalar divisor -> multiply by the fp32 reciprocal).
+    """
     vt = v.transpose(1, 2).float()
-    scale = vt.abs().amax(dim=(2, 3)).float() / 448.0
+    scale = vt.abs().amax(dim=(2, 3)).float() * torch.tensor(1.0 / 448.0, dtype=torch.float32)
     scale = scale.clamp_min(1e-12)
     vq = (vt / scale[:, :, None, None]).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
     return vq.view(torch.uint8).numpy(), scale.numpy()
@@ -87,3 +91,15 @@ def test_quantize_round_trip_error_bound():
     ref = v.float().numpy().transpose(0, 2, 1, 3)
     rel = np.linalg.norm(deq - ref) / np.linalg.norm(ref)
     assert rel < 0.03
+
+
+def test_scale_uses_reciprocal_multiply_not_division():
+    """The two roundings differ for some amax: the oracle must follow the reciprocal form."""
+    amax = np.float32(np.linspace(0.5, 8.0, 20001))
+    inv = np.float32(1.0) / np.float32(448.0)
+    assert (amax * inv != amax / np.float32(448.0)).any()
+    v = np.zeros((1, 1, 1, 2), dtype=np.float32)
+    for a in amax[:200]:
+        v[0, 0, 0, 0] = a
+        _, scale = of.quantize_per_head(v)
+        assert scale[0, 0] == max(a * inv, np.float32(1e-12))
