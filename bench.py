@@ -42,7 +42,22 @@ def parse():
                     help="target duration of the CPU baseline sample (0 disables it)")
     ap.add_argument("--only", choices=["t2i_1024", "edit_768"], default=None,
                     help="time one shape only (profiling aid; the default times both)")
+    ap.add_argument("--copy-calibration-mb", type=int, default=0,
+                    help="instead of the benchmark, run 5 plain device copies of this many MiB "
+                         "(reference point for the FETCH_SIZE / WRITE_SIZE counters) and exit")
     return ap.parse_args()
+
+
+def copy_calibration(mb: int) -> None:
+    import torch
+
+    n = mb * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes_per_copy": n * 4, "copies": 5}), flush=True)
 
 
 def cpu_model() -> str:
@@ -101,6 +116,10 @@ def main():
               "(per-head work shards without communication, but no multi-GPU path is built)",
               file=sys.stderr, flush=True)
         sys.exit(2)
+
+    if args.copy_calibration_mb > 0:
+        copy_calibration(args.copy_calibration_mb)
+        return
 
     import torch
 

@@ -138,6 +138,55 @@ __device__ __forceinline__ i16x4 lds_read_tr16(const char* p) {
       (__attribute__((address_space(3))) i16x4*)(p));
 }
 
+// Wave-uniform buffer resource over [base, base + bytes); loads at or past
+// `bytes` return zeros (this zero-fills the rows past a segment's end).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const char* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), (short)0, max(bytes, 0), 0x00020000);
+}
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// 64 lanes x 16 B, global -> LDS without passing through registers
+// (buffer_load_dwordx4 ... lds): lane l's 16 bytes land at lds_dst + 16*l.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, char* lds_dst, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds_dst, 16, voff, 0, 0, 0);
+}
+
+__device__ __forceinline__ u32x4 lds128(const char* p) { return *reinterpret_cast<const u32x4*>(p); }
+
+// Per-lane source offset of the direct-to-LDS tile copy.  Instruction r of wave
+// w fills LDS bytes [R0*ROWB, R0*ROWB + 1024) with R0 = (1024/ROWB)*(NWAVES*r + w):
+// lane l writes row R0 + l/CH, physical chunk l%CH, which must hold logical
+// chunk (l%CH) ^ swz(row).  swz() only looks at row bits 0-3 and R0 changes by
+// multiples of 16 between instructions, so the offset does not depend on r.
+template <int D>
+__device__ __forceinline__ uint32_t dma_lane_offset(int lane, int wave, int row_stride) {
+  constexpr int CH = D / 8;
+  constexpr int ROWS_PER_KB = 1024 / (D * 2);
+  const int r_in = lane / CH;
+  const int row = ROWS_PER_KB * wave + r_in;
+  const int c = (lane % CH) ^ swz<CH>(row);
+  return (uint32_t)(r_in * row_stride + c * 16);
+}
+
+// One KV tile of K (or bf16 V) starting at `tile` (its first row), rows
+// `row_stride` bytes apart; rows >= n_in are zero-filled.  Byte offsets inside
+// a tile fit in 31 bits (checked on the host: BN * row_stride < 2^31).
+template <int D>
+__device__ __forceinline__ void dma_tile(const char* tile, int row_stride, int n_in, char* lds_tile, int wave,
+                                         uint32_t lane_off) {
+  constexpr int ROWB = D * 2;
+  constexpr int ROWS_PER_KB = 1024 / ROWB;
+  constexpr int PER_WAVE = BN * ROWB / (NWAVES * 1024);
+#pragma unroll
+  for (int r = 0; r < PER_WAVE; ++r) {
+    const int R0 = ROWS_PER_KB * (NWAVES * r + wave);
+    const int rows = n_in - R0;
+    const int bytes = rows > 0 ? (rows - 1) * row_stride + ROWB : 0;
+    dma16(make_rsrc(tile + R0 * row_stride, bytes), lds_tile + R0 * ROWB, lane_off);
+  }
+}
+
 template <int D, bool FP16, bool V_FP8>
 __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params p) {
   constexpr int CH = D / 8;              // 16-byte chunks per row (8 elements)
@@ -146,17 +195,24 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params p) {
   constexpr int DBLK = D / 32;           // 32-row blocks of O^T
   constexpr int NBLK = BN / 32;          // 32-key blocks of S^T
   constexpr int SLABS = BN / 16;         // k-slabs of O^T = V^T.P^T
-  constexpr int LOADS = BN * CH / NTHREADS;
   constexpr int TILE_BYTES = BN * ROWB;
-  static_assert(LOADS * NTHREADS == BN * CH, "tile must split evenly over the workgroup");
+  constexpr int STAGE_BYTES = 2 * TILE_BYTES;
+  constexpr int CH8 = D / 16;            // 16-byte chunks per fp8 row
+  constexpr int F8_LOADS = BN * D / (NTHREADS * 16);
+  constexpr float TAU = 8.0f;            // rescale only when a row max grows by more than 2^8
+  static_assert(NBLK == 2, "the S^T code below holds two 32-key blocks");
+  static_assert(F8_LOADS >= 1 && F8_LOADS * NTHREADS * 16 == BN * D, "fp8 tile split");
 
-  __shared__ u32x4 smem[2 * 2 * TILE_BYTES / 16];  // [stage][K, V][BN x D]
-  __shared__ int sred[2 * NWAVES];
+  __shared__ u32x4 smem[2 * STAGE_BYTES / 16];  // [stage][K, V][BN x D] bf16
+  __shared__ uint32_t skv[2][BN / 4];           // key_valid bytes of each stage's tile (4 per word)
+  __shared__ int sred[NWAVES];
   char* const sbase = reinterpret_cast<char*>(smem);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  // wave-uniform values go through readfirstlane so that the compiler keeps
+  // them (and the buffer resources built from them) in SGPRs
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hf = lane >> 5;   // lane half: keys 4*hf.. of each 8-key group
   const int l32 = lane & 31;
 
@@ -175,8 +231,8 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params p) {
   const int m = mb * BM + wave * 32 + l32;  // this lane's query row
   const bool live = m < p.SQ;
 
-  // ---- causal lengths: this row's L, the block's max (dead rows count as -1,
-  // triton_attention.py:82-83) and the wave's min over live rows.
+  // ---- causal lengths: this row's L; the block max (dead rows count as -1,
+  // triton_attention.py:82-83); the wave's min and max over live rows.
   int Lrow = p.KV - 1;
   if (!p.uniform) Lrow = live ? p.L[m] : -1;
   int lmax = live ? Lrow : -1;
@@ -191,7 +247,9 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params p) {
   int Lmax = sred[0];
 #pragma unroll
   for (int w = 1; w < NWAVES; ++w) Lmax = max(Lmax, sred[w]);
-  const int wave_minL = lmin;
+  Lmax = __builtin_amdgcn_readfirstlane(Lmax);
+  const int wave_minL = __builtin_amdgcn_readfirstlane(lmin);
+  const int wave_maxL = __builtin_amdgcn_readfirstlane(lmax);
 
   // ---- KV-tile schedule: tile t of a segment starting at absolute key s0 is
   // visited iff s0 + t*BN <= Lmax (segment-local tiles, triton_attention.py:97-124).
@@ -202,7 +260,7 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params p) {
   if (Lmax >= s1) run1 = min(cdiv_i(p.SN, BN), (Lmax - s1) / BN + 1);
   const int T = run0 + run1;
 
-  // ---- per-(b,h) bases
+  // ---- per-(b,h) segment bases (bytes) and row strides
   constexpr int VC_ES = V_FP8 ? 1 : 2;
   const char* const qb = p.q + (b * p.sq[0] + h * p.sq[2]) * 2;
   const char* const knb = p.k_new + (b * p.skn[0] + h * p.skn[2]) * 2;
@@ -215,9 +273,18 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params p) {
     vcb = p.v_cache + (b * p.svc[0] + h * p.svc[2]) * VC_ES;
     if constexpr (V_FP8) vsc = p.v_scale[b * p.H + h];
   }
-  const int64_t kns = p.skn[1] * 2, vns = p.svn[1] * 2;
-  const int64_t kcs = p.skc[1] * 2, vcs = p.svc[1] * VC_ES;
+  const int kns = (int)(p.skn[1] * 2), vns = (int)(p.svn[1] * 2);
+  const int kcs = (int)(p.skc[1] * 2), vcs = (int)(p.svc[1] * VC_ES);
   const float qk_scale = p.qk_scale;
+
+  // lane offsets of the tile copies, per segment and tensor
+  const uint32_t koff_new = dma_lane_offset<D>(lane, wave, kns);
+  const uint32_t voff_new = dma_lane_offset<D>(lane, wave, vns);
+  uint32_t koff_c = 0, voff_c = 0;
+  if (p.has_cache) {
+    koff_c = dma_lane_offset<D>(lane, wave, kcs);
+    if constexpr (!V_FP8) voff_c = dma_lane_offset<D>(lane, wave, vcs);
+  }
 
   // ---- Q as the B operand of S^T = K.Q^T: lane holds Q[m, 16j + 8hf .. +8]
   u32x4 qreg[KSTEPS];
@@ -230,173 +297,210 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params p) {
     }
   }
 
-  // ---- global -> register staging of one KV tile, register -> LDS store
-  u32x4 kst[LOADS], vst[LOADS];
-  auto load_tile = [&](int g) {
+  // ---- LDS operand offsets inside a stage (lane constants)
+  const int swk = swz<CH>(l32);  // rows l32 and l32 + 32 share it
+  int koffs[KSTEPS];
+#pragma unroll
+  for (int j = 0; j < KSTEPS; ++j) koffs[j] = l32 * ROWB + (((2 * j + hf) ^ swk) << 4);
+  const int j16 = lane & 15;
+  const int rq = 4 * hf + (j16 >> 2);   // V^T read rows: 32*(s>>1) + 16*(s&1) + rq (+8)
+  const int colq = 16 * ((lane >> 4) & 1) + 4 * (j16 & 3);
+  int voffs[2][DBLK];
+#pragma unroll
+  for (int db = 0; db < DBLK; ++db) {
+    const int col = db * 32 + colq;
+    voffs[0][db] = TILE_BYTES + rq * ROWB + (((col >> 3) ^ swz<CH>(rq)) << 4) + ((col & 7) << 1);
+    voffs[1][db] = TILE_BYTES + (rq + 8) * ROWB + (((col >> 3) ^ swz<CH>(rq + 8)) << 4) + ((col & 7) << 1);
+  }
+
+  // fp8 slab V goes through registers: two 16-fp8 chunks per thread per tile
+  u32x4 f8reg[F8_LOADS];
+  uint32_t kvbyte = 0;
+
+  auto issue_tile = [&](int g, int stage) {
     const bool seg0 = g < run0;
     const int t = seg0 ? g : g - run0;
-    const int seg_len = seg0 ? p.P : p.SN;
-    const char* kbase = seg0 ? kcb : knb;
-    const char* vbase = seg0 ? vcb : vnb;
-    const int64_t ks = seg0 ? kcs : kns;
-    const int64_t vs = seg0 ? vcs : vns;
+    const int row0 = t * BN;
+    const int n_in = (seg0 ? p.P : p.SN) - row0;
+    char* kd = sbase + stage * STAGE_BYTES;
+    if (seg0) {
+      dma_tile<D>(kcb + (int64_t)row0 * kcs, kcs, n_in, kd, wave, koff_c);
+      if constexpr (V_FP8) {
+        const char* tb = vcb + (int64_t)row0 * vcs;
+        const auto rs = make_rsrc(tb, n_in > 0 ? (n_in - 1) * vcs + D : 0);
 #pragma unroll
-    for (int r = 0; r < LOADS; ++r) {
-      const int qd = r * NTHREADS + tid;
-      const int n = qd / CH, c = qd % CH;
-      const int nl = t * BN + n;
-      if (nl < seg_len) {
-        kst[r] = *reinterpret_cast<const u32x4*>(kbase + (int64_t)nl * ks + c * 16);
-        if (V_FP8 && seg0) {
-          const u32x2 w = *reinterpret_cast<const u32x2*>(vbase + (int64_t)nl * vs + c * 8);
-          vst[r] = u32x4{w.x, w.y, 0u, 0u};
-        } else {
-          vst[r] = *reinterpret_cast<const u32x4*>(vbase + (int64_t)nl * vs + c * 16);
+        for (int i = 0; i < F8_LOADS; ++i) {
+          const int qd = i * NTHREADS + tid;
+          const int row = qd / CH8, c16 = qd % CH8;
+          f8reg[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                    rs, (uint32_t)(row * vcs + c16 * 16), 0, 0));
         }
       } else {
-        kst[r] = u32x4{0u, 0u, 0u, 0u};
-        vst[r] = u32x4{0u, 0u, 0u, 0u};
+        dma_tile<D>(vcb + (int64_t)row0 * vcs, vcs, n_in, kd + TILE_BYTES, wave, voff_c);
+      }
+    } else {
+      dma_tile<D>(knb + (int64_t)row0 * kns, kns, n_in, kd, wave, koff_new);
+      dma_tile<D>(vnb + (int64_t)row0 * vns, vns, n_in, kd + TILE_BYTES, wave, voff_new);
+    }
+    if (p.has_key_valid && tid < BN) {
+      // one byte per thread so that bytes past the segment end read as 0 (invalid)
+      const int kv0 = (seg0 ? 0 : s1) + row0;
+      const auto rs = make_rsrc(reinterpret_cast<const char*>(p.key_valid) + b * p.svalid_b + kv0, n_in);
+      kvbyte = __builtin_amdgcn_raw_buffer_load_b8(rs, (uint32_t)tid, 0, 0);
+    }
+  };
+  // register-staged parts of a tile: fp8 V dequantised to bf16, key_valid bytes
+  auto finish_tile = [&](int g, int stage) {
+    char* vd = sbase + stage * STAGE_BYTES + TILE_BYTES;
+    if constexpr (V_FP8) {
+      if (g < run0) {
+#pragma unroll
+        for (int i = 0; i < F8_LOADS; ++i) {
+          const int qd = i * NTHREADS + tid;
+          const int row = qd / CH8, c16 = qd % CH8;
+          const u32x4 w = f8reg[i];
+          const u32x4 lo = dequant_fp8x8(w.x, w.y, vsc);  // elements 16*c16 .. +7
+          const u32x4 hi = dequant_fp8x8(w.z, w.w, vsc);  // elements 16*c16+8 .. +15
+          *reinterpret_cast<u32x4*>(vd + row * ROWB + (((2 * c16) ^ swz<CH>(row)) << 4)) = lo;
+          *reinterpret_cast<u32x4*>(vd + row * ROWB + (((2 * c16 + 1) ^ swz<CH>(row)) << 4)) = hi;
+        }
       }
     }
-  };
-  auto store_tile = [&](int g, int stage) {
-    const bool fp8 = V_FP8 && (g < run0);
-    char* kd = sbase + stage * 2 * TILE_BYTES;
-    char* vd = kd + TILE_BYTES;
-#pragma unroll
-    for (int r = 0; r < LOADS; ++r) {
-      const int qd = r * NTHREADS + tid;
-      const int n = qd / CH, c = qd % CH;
-      const int off = n * ROWB + ((c ^ swz<CH>(n)) << 4);
-      *reinterpret_cast<u32x4*>(kd + off) = kst[r];
-      u32x4 vv = vst[r];
-      if (fp8) vv = dequant_fp8x8(vv.x, vv.y, vsc);  // zero codes stay zero
-      *reinterpret_cast<u32x4*>(vd + off) = vv;
-    }
+    if (p.has_key_valid && tid < BN) reinterpret_cast<uint8_t*>(skv[stage])[tid] = (uint8_t)kvbyte;
   };
 
-  float m_run = -INFINITY;  // running row max, exp2 domain (scaled)
+  float m_run = -INFINITY;  // exp2 reference point of each row (scaled units)
   float l_run = 0.0f;       // this lane half's share of the running row sum
   f32x16 oacc[DBLK];
 #pragma unroll
   for (int db = 0; db < DBLK; ++db) oacc[db] = f32x16{};
 
-  if (T > 0) {
-    load_tile(0);
-    store_tile(0, 0);
-  }
-  __syncthreads();
-
-  for (int g = 0; g < T; ++g) {
-    const bool has_next = g + 1 < T;
-    if (has_next) load_tile(g + 1);
-
-    const char* kS = sbase + (g & 1) * 2 * TILE_BYTES;
-    const char* vS = kS + TILE_BYTES;
-
-    // S^T[n, m] = sum_d K[n, d] Q[m, d]; lane holds m = l32, n = 8(i/4) + 4hf + i%4
-    f32x16 sacc[NBLK];
-#pragma unroll
-    for (int nb = 0; nb < NBLK; ++nb) {
-      sacc[nb] = f32x16{};
-      const int n = nb * 32 + l32;
-      const char* krow = kS + n * ROWB;
-#pragma unroll
-      for (int j = 0; j < KSTEPS; ++j) {
-        const int c = 2 * j + hf;
-        const u32x4 a = *reinterpret_cast<const u32x4*>(krow + ((c ^ swz<CH>(n)) << 4));
-        sacc[nb] = mfma32<FP16>(a, qreg[j], sacc[nb]);
-      }
-    }
-
-    // mask: segment tail, kv <= L[row], key_valid (triton_attention.py:126-144)
+  auto compute_tile = [&](int g, int stage) {
+    const char* kS = sbase + stage * STAGE_BYTES;
     const bool seg0 = g < run0;
     const int t = seg0 ? g : g - run0;
     const int n_in = (seg0 ? p.P : p.SN) - t * BN;  // keys of this tile inside its segment
     const int kv0 = (seg0 ? 0 : s1) + t * BN;        // absolute index of the tile's first key
-    const bool full = (n_in >= BN) && (kv0 + BN - 1 <= wave_minL) && !p.has_key_valid;
-    if (!full) {
-      const uint8_t* kvrow = p.has_key_valid ? p.key_valid + (int64_t)b * p.svalid_b : nullptr;
+    if (kv0 > wave_maxL) return;                     // no row of this wave sees the tile
+
+    // S^T[n, m] = sum_d K[n, d] Q[m, d]; lane holds m = l32, n = 8(i/4) + 4hf + i%4 (+32)
+    f32x16 sa = f32x16{}, sb = f32x16{};
+    {
+      u32x4 ka0 = lds128(kS + koffs[0]);
+      u32x4 kb0 = lds128(kS + koffs[0] + 32 * ROWB);
 #pragma unroll
-      for (int nb = 0; nb < NBLK; ++nb) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int n = nb * 32 + 8 * (i >> 2) + 4 * hf + (i & 3);
-          const int kv = kv0 + n;
-          bool ok = (n < n_in) && (kv <= Lrow);
-          if (kvrow != nullptr && ok) ok = kvrow[kv] != 0;
-          if (!ok) sacc[nb][i] = -INFINITY;
+      for (int j = 0; j < KSTEPS; ++j) {
+        u32x4 ka1, kb1;
+        if (j + 1 < KSTEPS) {
+          ka1 = lds128(kS + koffs[j + 1]);
+          kb1 = lds128(kS + koffs[j + 1] + 32 * ROWB);
+        }
+        sa = mfma32<FP16>(ka0, qreg[j], sa);
+        sb = mfma32<FP16>(kb0, qreg[j], sb);
+        if (j + 1 < KSTEPS) {
+          ka0 = ka1;
+          kb0 = kb1;
         }
       }
     }
 
-    // online softmax, exp2 domain (triton_attention.py:146-152)
-    float mx = -INFINITY;
+    // mask: segment tail, kv <= L[row], key_valid (triton_attention.py:126-144)
+    const bool full = (n_in >= BN) && (kv0 + BN - 1 <= wave_minL) && !p.has_key_valid;
+    if (!full) {
+      const int lim = min(Lrow - kv0, n_in - 1) - 4 * hf;  // allowed: n_local - 4hf <= lim
+      uint32_t kvw[8];
+      if (p.has_key_valid) {
 #pragma unroll
-    for (int nb = 0; nb < NBLK; ++nb)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sacc[nb][i]);
-    mx = pair_max(mx);
-    const float m_new = fmaxf(m_run, mx * qk_scale);
-    const float m_safe = (m_new == -INFINITY) ? 0.0f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_safe);
-    float rs = 0.0f;
-#pragma unroll
-    for (int nb = 0; nb < NBLK; ++nb)
+        for (int q = 0; q < 8; ++q) kvw[q] = skv[stage][q * 2 + hf];  // bytes of keys 8q + 4hf .. +3
+      }
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[nb][i], qk_scale, -m_safe));
-        sacc[nb][i] = e;
-        rs += e;
+        const int na = 8 * (i >> 2) + (i & 3);
+        bool oka = na <= lim, okb = na + 32 <= lim;
+        if (p.has_key_valid) {
+          oka = oka && ((kvw[i >> 2] >> (8 * (i & 3))) & 0xffu) != 0;
+          okb = okb && ((kvw[4 + (i >> 2)] >> (8 * (i & 3))) & 0xffu) != 0;
+        }
+        sa[i] = oka ? sa[i] : -INFINITY;
+        sb[i] = okb ? sb[i] : -INFINITY;
       }
-    l_run = l_run * alpha + rs;
-    m_run = m_new;
+    }
+
+    // online softmax in the exp2 domain (triton_attention.py:146-152); the
+    // reference point moves only when a row max grows by more than TAU, so
+    // p <= 2^TAU and the acc rescale is skipped on most tiles
+    float mx = fmaxf(sa[0], sb[0]);
+#pragma unroll
+    for (int i = 1; i < 16; ++i) mx = fmaxf(fmaxf(mx, sa[i]), sb[i]);
+    mx = pair_max(mx) * qk_scale;
+    if (__any(mx > m_run + TAU)) {
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = (m_new == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < DBLK; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) oacc[db][i] *= alpha;
+      m_run = m_new;
+    }
+    const float m_safe = (m_run == -INFINITY) ? 0.0f : m_run;
+    float rs = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      sa[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sa[i], qk_scale, -m_safe));
+      sb[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sb[i], qk_scale, -m_safe));
+      rs += sa[i];
+      rs += sb[i];
+    }
+    l_run += rs;
 
     // P^T as the B operand: slab s uses registers 8*(s%2).. of block s/2
     u32x4 pb[SLABS];
 #pragma unroll
     for (int s = 0; s < SLABS; ++s) {
-      const int nb = s >> 1, i0 = (s & 1) * 8;
-      pb[s].x = pack2<FP16>(sacc[nb][i0 + 0], sacc[nb][i0 + 1]);
-      pb[s].y = pack2<FP16>(sacc[nb][i0 + 2], sacc[nb][i0 + 3]);
-      pb[s].z = pack2<FP16>(sacc[nb][i0 + 4], sacc[nb][i0 + 5]);
-      pb[s].w = pack2<FP16>(sacc[nb][i0 + 6], sacc[nb][i0 + 7]);
+      const f32x16& src = (s >> 1) ? sb : sa;
+      const int i0 = (s & 1) * 8;
+      pb[s].x = pack2<FP16>(src[i0 + 0], src[i0 + 1]);
+      pb[s].y = pack2<FP16>(src[i0 + 2], src[i0 + 3]);
+      pb[s].z = pack2<FP16>(src[i0 + 4], src[i0 + 5]);
+      pb[s].w = pack2<FP16>(src[i0 + 6], src[i0 + 7]);
     }
 
-    // acc *= alpha, skipped when every row of the wave keeps its max (alpha == 1 exactly)
-    if (__any(alpha != 1.0f)) {
+    // O^T[d, m] += sum_n V[n, d] P[m, n]; the V^T operand comes from the LDS
+    // transpose read: source lane j of each 16-lane group reads row base + j/4,
+    // columns d0 + 4(j%4)..+3, and receives column d0 + j of rows base..base+3
 #pragma unroll
-      for (int db = 0; db < DBLK; ++db)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) oacc[db][i] *= alpha;
-    }
-
-    // O^T[d, m] += sum_n V[n, d] P[m, n]; V^T operand via the LDS transpose read:
-    // source lane j of each 16-lane group reads row base + j/4, columns d0 + 4(j%4)..+3
-    {
-      const int j16 = lane & 15;
-      const int colq = 16 * ((lane >> 4) & 1) + 4 * (j16 & 3);
+    for (int s = 0; s < SLABS; ++s) {
+      const int soff = ((s >> 1) * 32 + 16 * (s & 1)) * ROWB;
 #pragma unroll
       for (int db = 0; db < DBLK; ++db) {
-        const int col = db * 32 + colq;
-#pragma unroll
-        for (int s = 0; s < SLABS; ++s) {
-          const int r0 = (s >> 1) * 32 + 16 * (s & 1) + 4 * hf + (j16 >> 2);
-          const int r1 = r0 + 8;
-          const char* a0 = vS + r0 * ROWB + (((col >> 3) ^ swz<CH>(r0)) << 4) + ((col & 7) << 1);
-          const char* a1 = vS + r1 * ROWB + (((col >> 3) ^ swz<CH>(r1)) << 4) + ((col & 7) << 1);
-          const i16x4 x0 = lds_read_tr16(a0);
-          const i16x4 x1 = lds_read_tr16(a1);
-          const u32x2 w0 = __builtin_bit_cast(u32x2, x0);
-          const u32x2 w1 = __builtin_bit_cast(u32x2, x1);
-          const u32x4 a = u32x4{w0.x, w0.y, w1.x, w1.y};
-          oacc[db] = mfma32<FP16>(a, pb[s], oacc[db]);
-        }
+        const i16x4 x0 = lds_read_tr16(kS + voffs[0][db] + soff);
+        const i16x4 x1 = lds_read_tr16(kS + voffs[1][db] + soff);
+        const u32x2 w0 = __builtin_bit_cast(u32x2, x0);
+        const u32x2 w1 = __builtin_bit_cast(u32x2, x1);
+        oacc[db] = mfma32<FP16>(u32x4{w0.x, w0.y, w1.x, w1.y}, pb[s], oacc[db]);
       }
     }
+  };
 
-    if (has_next) store_tile(g + 1, (g + 1) & 1);
+  if (T > 0) {
+    issue_tile(0, 0);
+    finish_tile(0, 0);
+  }
+  __syncthreads();
+
+  for (int g = 0; g < T; g += 2) {
+    // even tile from stage 0, odd tile from stage 1 (constant LDS offsets)
+    if (g + 1 < T) issue_tile(g + 1, 1);
+    compute_tile(g, 0);
+    if (g + 1 < T) finish_tile(g + 1, 1);
     __syncthreads();
+    if (g + 1 < T) {
+      if (g + 2 < T) issue_tile(g + 2, 0);
+      compute_tile(g + 1, 1);
+      if (g + 2 < T) finish_tile(g + 2, 0);
+      __syncthreads();
+    }
   }
 
   // ---- epilogue: out = l > 0 ? acc / l : 0 (triton_attention.py:166-168)
@@ -486,7 +590,7 @@ const char* qik_strerror(int status) {
     case QIK_ERR_SHAPE: return "negative or oversized B/SQ/SN/P/H";
     case QIK_ERR_CACHE: return "cache flag, P and cache pointers are inconsistent";
     case QIK_ERR_FP8_SCALE: return "fp8 cache V needs the cache, a v_scale pointer and bf16 q/k/v";
-    case QIK_ERR_ALIGN: return "pointers and b/s/h strides must be multiples of 8 elements (16 B rows chunks)";
+    case QIK_ERR_ALIGN: return "pointers and b/s/h strides must be multiples of 8 elements, and K/V row strides at least D";
     case QIK_ERR_LAUNCH: return "HIP kernel launch failed";
     case QIK_ERR_SEGMENTS: return "segments need 0 <= start <= end, and 0 <= prefix_end <= seq_len";
     case QIK_ERR_DEVICE: return "HIP device query failed";
@@ -539,6 +643,15 @@ int qik_attn_validate(const qik_attn_args* a) {
     if (!qik::stride_ok(a->stride_k_new, a->B, a->SN, a->H, 8)) return QIK_ERR_ALIGN;
     if (!qik::stride_ok(a->stride_v_new, a->B, a->SN, a->H, 8)) return QIK_ERR_ALIGN;
   }
+  // a KV tile's byte offsets must fit in 31 bits (the tile copies use 32-bit
+  // buffer offsets): BN * row stride < 2^31
+  const int64_t tile_lim = ((int64_t)1 << 31) / qik::BN;
+  if (a->stride_k_new[1] * 2 >= tile_lim || a->stride_v_new[1] * 2 >= tile_lim) return QIK_ERR_SHAPE;
+  if (has_cache && (a->stride_k_cache[1] * 2 >= tile_lim || a->stride_v_cache[1] * 2 >= tile_lim)) return QIK_ERR_SHAPE;
+  // K/V rows must not overlap (the tile copies zero-fill a segment tail through
+  // buffer bounds that assume row_stride >= D)
+  if (a->SN > 1 && (a->stride_k_new[1] < a->D || a->stride_v_new[1] < a->D)) return QIK_ERR_ALIGN;
+  if (has_cache && a->P > 1 && (a->stride_k_cache[1] < a->D || a->stride_v_cache[1] < a->D)) return QIK_ERR_ALIGN;
   if (has_cache) {
     if (!qik::aligned_to(a->k_cache, 16)) return QIK_ERR_ALIGN;
     if (!qik::aligned_to(a->v_cache, vfp8 ? 8 : 16)) return QIK_ERR_ALIGN;
