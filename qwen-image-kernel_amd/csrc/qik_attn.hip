@@ -32,6 +32,7 @@
 #include <string.h>
 #include <limits.h>
 #include <algorithm>
+#include <type_traits>
 
 #include "qik_attn.h"
 
@@ -196,17 +197,23 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params p) {
   constexpr int NBLK = BN / 32;          // 32-key blocks of S^T
   constexpr int SLABS = BN / 16;         // k-slabs of O^T = V^T.P^T
   constexpr int TILE_BYTES = BN * ROWB;
-  constexpr int STAGE_BYTES = 2 * TILE_BYTES;
   constexpr int CH8 = D / 16;            // 16-byte chunks per fp8 row
   constexpr int F8_LOADS = BN * D / (NTHREADS * 16);
   constexpr float TAU = 8.0f;            // rescale only when a row max grows by more than 2^8
   static_assert(NBLK == 2, "the S^T code below holds two 32-key blocks");
   static_assert(F8_LOADS >= 1 && F8_LOADS * NTHREADS * 16 == BN * D, "fp8 tile split");
 
-  __shared__ u32x4 smem[2 * STAGE_BYTES / 16];  // [stage][K, V][BN x D] bf16
+  // K and V tiles of the two stages, each its own array: the compiler then
+  // knows that a tile copy into one stage cannot alias the operand reads of
+  // the other and does not wait for the copy before computing
+  __shared__ u32x4 sk0[TILE_BYTES / 16];
+  __shared__ u32x4 sk1[TILE_BYTES / 16];
+  __shared__ u32x4 sv0[TILE_BYTES / 16];
+  __shared__ u32x4 sv1[TILE_BYTES / 16];
   __shared__ uint32_t skv[2][BN / 4];           // key_valid bytes of each stage's tile (4 per word)
   __shared__ int sred[NWAVES];
-  char* const sbase = reinterpret_cast<char*>(smem);
+  char* const kst[2] = {reinterpret_cast<char*>(sk0), reinterpret_cast<char*>(sk1)};
+  char* const vst[2] = {reinterpret_cast<char*>(sv0), reinterpret_cast<char*>(sv1)};
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -309,8 +316,8 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params p) {
 #pragma unroll
   for (int db = 0; db < DBLK; ++db) {
     const int col = db * 32 + colq;
-    voffs[0][db] = TILE_BYTES + rq * ROWB + (((col >> 3) ^ swz<CH>(rq)) << 4) + ((col & 7) << 1);
-    voffs[1][db] = TILE_BYTES + (rq + 8) * ROWB + (((col >> 3) ^ swz<CH>(rq + 8)) << 4) + ((col & 7) << 1);
+    voffs[0][db] = rq * ROWB + (((col >> 3) ^ swz<CH>(rq)) << 4) + ((col & 7) << 1);
+    voffs[1][db] = (rq + 8) * ROWB + (((col >> 3) ^ swz<CH>(rq + 8)) << 4) + ((col & 7) << 1);
   }
 
   // fp8 slab V goes through registers: two 16-fp8 chunks per thread per tile
@@ -322,7 +329,8 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params p) {
     const int t = seg0 ? g : g - run0;
     const int row0 = t * BN;
     const int n_in = (seg0 ? p.P : p.SN) - row0;
-    char* kd = sbase + stage * STAGE_BYTES;
+    char* kd = kst[stage];
+    char* vdst = vst[stage];
     if (seg0) {
       dma_tile<D>(kcb + (int64_t)row0 * kcs, kcs, n_in, kd, wave, koff_c);
       if constexpr (V_FP8) {
@@ -336,11 +344,11 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params p) {
                                                     rs, (uint32_t)(row * vcs + c16 * 16), 0, 0));
         }
       } else {
-        dma_tile<D>(vcb + (int64_t)row0 * vcs, vcs, n_in, kd + TILE_BYTES, wave, voff_c);
+        dma_tile<D>(vcb + (int64_t)row0 * vcs, vcs, n_in, vdst, wave, voff_c);
       }
     } else {
       dma_tile<D>(knb + (int64_t)row0 * kns, kns, n_in, kd, wave, koff_new);
-      dma_tile<D>(vnb + (int64_t)row0 * vns, vns, n_in, kd + TILE_BYTES, wave, voff_new);
+      dma_tile<D>(vnb + (int64_t)row0 * vns, vns, n_in, vdst, wave, voff_new);
     }
     if (p.has_key_valid && tid < BN) {
       // one byte per thread so that bytes past the segment end read as 0 (invalid)
@@ -351,7 +359,7 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params p) {
   };
   // register-staged parts of a tile: fp8 V dequantised to bf16, key_valid bytes
   auto finish_tile = [&](int g, int stage) {
-    char* vd = sbase + stage * STAGE_BYTES + TILE_BYTES;
+    char* vd = vst[stage];
     if constexpr (V_FP8) {
       if (g < run0) {
 #pragma unroll
@@ -376,7 +384,8 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params p) {
   for (int db = 0; db < DBLK; ++db) oacc[db] = f32x16{};
 
   auto compute_tile = [&](int g, int stage) {
-    const char* kS = sbase + stage * STAGE_BYTES;
+    const char* kS = kst[stage];
+    const char* vS = vst[stage];
     const bool seg0 = g < run0;
     const int t = seg0 ? g : g - run0;
     const int n_in = (seg0 ? p.P : p.SN) - t * BN;  // keys of this tile inside its segment
@@ -474,8 +483,8 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params p) {
       const int soff = ((s >> 1) * 32 + 16 * (s & 1)) * ROWB;
 #pragma unroll
       for (int db = 0; db < DBLK; ++db) {
-        const i16x4 x0 = lds_read_tr16(kS + voffs[0][db] + soff);
-        const i16x4 x1 = lds_read_tr16(kS + voffs[1][db] + soff);
+        const i16x4 x0 = lds_read_tr16(vS + voffs[0][db] + soff);
+        const i16x4 x1 = lds_read_tr16(vS + voffs[1][db] + soff);
         const u32x2 w0 = __builtin_bit_cast(u32x2, x0);
         const u32x2 w1 = __builtin_bit_cast(u32x2, x1);
         oacc[db] = mfma32<FP16>(u32x4{w0.x, w0.y, w1.x, w1.y}, pb[s], oacc[db]);
