@@ -60,6 +60,27 @@ def copy_calibration(mb: int) -> None:
     print(json.dumps({"copy_calibration_bytes_per_copy": n * 4, "copies": 5}), flush=True)
 
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "attn_fwd_traffic.txt")
+
+
+def profiled_traffic(name: str):
+    """HBM bytes per launch of the kernel for one shape, from the committed counter summary.
+
+    The counters (FETCH_SIZE, WRITE_SIZE, each scaled by a plain-copy
+    calibration) come from separate rocprofv3 --pmc runs of this script; the
+    summary lists '<shape> <bytes>' lines.  None when the file or shape is absent.
+    """
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                parts = line.split()
+                if len(parts) == 2 and not line.startswith("#") and parts[0] == name:
+                    return int(parts[1])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -230,7 +251,10 @@ def main():
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-            "traffic": None,
+            "traffic": profiled_traffic(dom),
+            "traffic_source": "profiles/attn_fwd_traffic.txt (rocprofv3 FETCH_SIZE/WRITE_SIZE, copy-calibrated)",
+            "algorithmic_flops_per_launch": dwl.flops(),
+            "compulsory_bytes_per_launch": dwl.min_bytes(),
         },
         "per_workload": per_workload,
         "cpu_baseline": cpu,
