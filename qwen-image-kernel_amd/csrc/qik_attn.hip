@@ -155,36 +155,45 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, char* lds_dst, u
 
 __device__ __forceinline__ u32x4 lds128(const char* p) { return *reinterpret_cast<const u32x4*>(p); }
 
-// Per-lane source offset of the direct-to-LDS tile copy.  Instruction r of wave
-// w fills LDS bytes [R0*ROWB, R0*ROWB + 1024) with R0 = (1024/ROWB)*(NWAVES*r + w):
-// lane l writes row R0 + l/CH, physical chunk l%CH, which must hold logical
-// chunk (l%CH) ^ swz(row).  swz() only looks at row bits 0-3 and R0 changes by
-// multiples of 16 between instructions, so the offset does not depend on r.
+// Per-lane source offset (from the tile's first row) of the direct-to-LDS tile
+// copy.  Instruction r of wave w of a group fills LDS bytes [R0*ROWB, R0*ROWB +
+// 1024) with R0 = (1024/ROWB)*(NWAVES*r + w): lane l writes row R0 + l/CH,
+// physical chunk l%CH, which must hold logical chunk (l%CH) ^ swz(row).
+// swz() only looks at row bits 0-3 and R0 changes by multiples of 16 between
+// instructions, so instruction r adds r * (1024/ROWB)*NWAVES rows to the offset
+// returned here (the one of r = 0).
 template <int D>
 __device__ __forceinline__ uint32_t dma_lane_offset(int lane, int wave, int row_stride) {
   constexpr int CH = D / 8;
   constexpr int ROWS_PER_KB = 1024 / (D * 2);
-  const int r_in = lane / CH;
-  const int row = ROWS_PER_KB * wave + r_in;
+  const int row = ROWS_PER_KB * wave + lane / CH;
   const int c = (lane % CH) ^ swz<CH>(row);
-  return (uint32_t)(r_in * row_stride + c * 16);
+  return (uint32_t)(row * row_stride + c * 16);
+}
+
+// Bytes of a tile's rows [0, min(n_in, BN)) when rows are `row_stride` apart
+// and `row_bytes` long: a buffer resource of that size zero-fills the rows past
+// a segment's end.  Fits in 31 bits (checked on the host: BN * row_stride < 2^31).
+__device__ __forceinline__ int tile_bytes(int n_in, int row_stride, int row_bytes) {
+  const int rows = min(n_in, BN);
+  return rows > 0 ? (rows - 1) * row_stride + row_bytes : 0;
 }
 
 // One KV tile of K (or bf16 V) starting at `tile` (its first row), rows
-// `row_stride` bytes apart; rows >= n_in are zero-filled.  Byte offsets inside
-// a tile fit in 31 bits (checked on the host: BN * row_stride < 2^31).
+// `row_stride` bytes apart; rows >= n_in are zero-filled.  One buffer resource
+// per tile; the instructions differ only in their VGPR offset and LDS target.
 template <int D>
 __device__ __forceinline__ void dma_tile(const char* tile, int row_stride, int n_in, char* lds_tile, int wave,
                                          uint32_t lane_off) {
   constexpr int ROWB = D * 2;
   constexpr int ROWS_PER_KB = 1024 / ROWB;
   constexpr int PER_WAVE = BN * ROWB / (NWAVES * 1024);
+  const auto rs = make_rsrc(tile, tile_bytes(n_in, row_stride, ROWB));
+  const uint32_t step = (uint32_t)(ROWS_PER_KB * NWAVES * row_stride);
 #pragma unroll
   for (int r = 0; r < PER_WAVE; ++r) {
     const int R0 = ROWS_PER_KB * (NWAVES * r + wave);
-    const int rows = n_in - R0;
-    const int bytes = rows > 0 ? (rows - 1) * row_stride + ROWB : 0;
-    dma16(make_rsrc(tile + R0 * row_stride, bytes), lds_tile + R0 * ROWB, lane_off);
+    dma16(rs, lds_tile + R0 * ROWB, lane_off + r * step);
   }
 }
 
@@ -197,15 +206,13 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params p) {
   constexpr int NBLK = BN / 32;          // 32-key blocks of S^T
   constexpr int SLABS = BN / 16;         // k-slabs of O^T = V^T.P^T
   constexpr int TILE_BYTES = BN * ROWB;
+  constexpr int STAGE_BYTES = 2 * TILE_BYTES;
   constexpr int CH8 = D / 16;            // 16-byte chunks per fp8 row
   constexpr int F8_LOADS = BN * D / (NTHREADS * 16);
   constexpr float TAU = 8.0f;            // rescale only when a row max grows by more than 2^8
   static_assert(NBLK == 2, "the S^T code below holds two 32-key blocks");
   static_assert(F8_LOADS >= 1 && F8_LOADS * NTHREADS * 16 == BN * D, "fp8 tile split");
 
-  // K and V tiles of the two stages, each its own array: the compiler then
-  // knows that a tile copy into one stage cannot alias the operand reads of
-  // the other and does not wait for the copy before computing
   __shared__ u32x4 sk0[TILE_BYTES / 16];
   __shared__ u32x4 sk1[TILE_BYTES / 16];
   __shared__ u32x4 sv0[TILE_BYTES / 16];
@@ -335,7 +342,7 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params p) {
       dma_tile<D>(kcb + (int64_t)row0 * kcs, kcs, n_in, kd, wave, koff_c);
       if constexpr (V_FP8) {
         const char* tb = vcb + (int64_t)row0 * vcs;
-        const auto rs = make_rsrc(tb, n_in > 0 ? (n_in - 1) * vcs + D : 0);
+        const auto rs = make_rsrc(tb, tile_bytes(n_in, vcs, D));
 #pragma unroll
         for (int i = 0; i < F8_LOADS; ++i) {
           const int qd = i * NTHREADS + tid;
@@ -353,7 +360,7 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params p) {
     if (p.has_key_valid && tid < BN) {
       // one byte per thread so that bytes past the segment end read as 0 (invalid)
       const int kv0 = (seg0 ? 0 : s1) + row0;
-      const auto rs = make_rsrc(reinterpret_cast<const char*>(p.key_valid) + b * p.svalid_b + kv0, n_in);
+      const auto rs = make_rsrc(reinterpret_cast<const char*>(p.key_valid) + b * p.svalid_b + kv0, min(n_in, BN));
       kvbyte = __builtin_amdgcn_raw_buffer_load_b8(rs, (uint32_t)tid, 0, 0);
     }
   };

@@ -6,7 +6,10 @@ loop and rounding points the bar is tighter (TIGHT_MAX).  Integer results
 (causal lengths, the visited-tile schedule) must be bit-exact.
 """
 
+import dataclasses
+
 import numpy as np
+
 import pytest
 import torch
 
@@ -343,6 +346,21 @@ def test_benchmark_shapes_all_heads_vs_torch_fp32(name):
     _flush(f"case all heads {name}")
     wl = wls.workload(name)
     inp = wls.make_inputs(wl, seed=77, device=DEV, gen_device="cuda")
+    out = _wl_run(wl, inp).float()
+    ref = _torch_fp32_reference(wl, inp)
+    d = (out - ref).abs()
+    assert torch.isfinite(out).all()
+    assert d.max().item() <= MAX_ABS and d.mean().item() <= MEAN_ABS, (d.max().item(), d.mean().item())
+
+
+@pytest.mark.parametrize("name,H", [("t2i_1024", 25), ("edit_768", 25), ("multiref_cfg", 13)])
+def test_odd_head_counts_all_heads_vs_torch_fp32(name, H):
+    """Head counts whose row blocks do not split evenly over the 8 XCDs (the
+    workgroup -> row block remap then gives some XCDs one more row block), at
+    full sequence length."""
+    _flush(f"case odd heads {name} H={H}")
+    wl = dataclasses.replace(wls.workload(name), H=H)
+    inp = wls.make_inputs(wl, seed=91, device=DEV, gen_device="cuda")
     out = _wl_run(wl, inp).float()
     ref = _torch_fp32_reference(wl, inp)
     d = (out - ref).abs()
