@@ -2,9 +2,12 @@
 
 Drop-in for the attention path of qwen_image_kernel: ``block_causal_flash_attention``
 (triton_attention.py:171) and the ``ContiguousKVCache`` prefix slab
-(kv_cache.py:63), computed by a hand-written HIP kernel behind a C ABI
-(include/qik_attn.h).  The package directory is ``qwen-image-kernel_amd/``;
-the top-level module ``qwen_image_kernel_amd.py`` imports it under this name.
+(kv_cache.py:63), computed by hand-written HIP kernels behind a C ABI
+(include/qik_attn.h), plus the steps on either side of the attention call:
+``fused_rms_norm_rope`` (triton_fused.py:75) and ``QwenImage21KernelProcessor``
+(processors.py:39) (include/qik_ops.h).  The package directory is
+``qwen-image-kernel_amd/``; the top-level module ``qwen_image_kernel_amd.py``
+imports it under this name.
 """
 
 from .attention import (  # noqa: F401
@@ -13,7 +16,9 @@ from .attention import (  # noqa: F401
     build_prefix_lengths,
     tile_schedule,
 )
+from .fused import fused_rms_norm_rope  # noqa: F401
 from .kv_cache import FP8_E4M3_MAX, ContiguousKVCache  # noqa: F401
+from .processors import QwenImage21KernelProcessor  # noqa: F401
 
 __all__ = [
     "block_causal_flash_attention",
@@ -22,4 +27,6 @@ __all__ = [
     "block_shape",
     "ContiguousKVCache",
     "FP8_E4M3_MAX",
+    "fused_rms_norm_rope",
+    "QwenImage21KernelProcessor",
 ]

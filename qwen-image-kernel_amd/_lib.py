@@ -1,4 +1,4 @@
-"""ctypes binding of the C ABI declared in include/qik_attn.h.
+"""ctypes binding of the C ABI declared in include/qik_attn.h and include/qik_ops.h.
 
 The shared library is built in-tree (``lib/libqik_attn.so`` next to this file)
 by ``build.py``.  There is no fallback: if the library is missing or fails to
@@ -85,6 +85,52 @@ class QikAttnArgs(ctypes.Structure):
     ]
 
 
+class QikRmsRopeArgs(ctypes.Structure):
+    """Mirror of ``struct qik_rms_rope_args`` (include/qik_ops.h)."""
+
+    _fields_ = [
+        ("abi_version", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("x", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("weight", ctypes.c_void_p),
+        ("cos", ctypes.c_void_p),
+        ("sin", ctypes.c_void_p),
+        ("B", ctypes.c_int64),
+        ("S", ctypes.c_int64),
+        ("H", ctypes.c_int64),
+        ("D", ctypes.c_int64),
+        ("stride_x", _i64x3),
+        ("stride_out", _i64x3),
+        ("eps", ctypes.c_float),
+        ("reserved0", ctypes.c_int32),
+    ]
+
+
+class QikSlabStoreArgs(ctypes.Structure):
+    """Mirror of ``struct qik_slab_store_args`` (include/qik_ops.h)."""
+
+    _fields_ = [
+        ("abi_version", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("v_fp8", ctypes.c_int32),
+        ("reserved0", ctypes.c_int32),
+        ("k", ctypes.c_void_p),
+        ("v", ctypes.c_void_p),
+        ("k_dst", ctypes.c_void_p),
+        ("v_dst", ctypes.c_void_p),
+        ("v_scale", ctypes.c_void_p),
+        ("B", ctypes.c_int64),
+        ("P", ctypes.c_int64),
+        ("H", ctypes.c_int64),
+        ("D", ctypes.c_int64),
+        ("stride_k", _i64x3),
+        ("stride_v", _i64x3),
+        ("stride_k_dst", _i64x3),
+        ("stride_v_dst", _i64x3),
+    ]
+
+
 # (name, restype, argtypes) of every exported entry point
 EXPORTS = (
     ("qik_abi_version", ctypes.c_int, ()),
@@ -102,6 +148,8 @@ EXPORTS = (
         ctypes.c_int,
         (ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p),
     ),
+    ("qik_rms_rope", ctypes.c_int, (ctypes.POINTER(QikRmsRopeArgs), ctypes.c_void_p)),
+    ("qik_slab_store", ctypes.c_int, (ctypes.POINTER(QikSlabStoreArgs), ctypes.c_void_p)),
 )
 
 _lock = threading.Lock()

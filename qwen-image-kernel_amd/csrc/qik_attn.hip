@@ -206,7 +206,6 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params p) {
   constexpr int NBLK = BN / 32;          // 32-key blocks of S^T
   constexpr int SLABS = BN / 16;         // k-slabs of O^T = V^T.P^T
   constexpr int TILE_BYTES = BN * ROWB;
-  constexpr int STAGE_BYTES = 2 * TILE_BYTES;
   constexpr int CH8 = D / 16;            // 16-byte chunks per fp8 row
   constexpr int F8_LOADS = BN * D / (NTHREADS * 16);
   constexpr float TAU = 8.0f;            // rescale only when a row max grows by more than 2^8

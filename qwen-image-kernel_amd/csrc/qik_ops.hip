@@ -1,0 +1,360 @@
+// Device steps beside the attention call of a Qwen-Image 2.1 layer on MI355X:
+// the per-head RMSNorm + RoPE that produces Q and K
+// (qwen_image_kernel/triton_fused.py:28-105) and the prefix-KV slab store with
+// per-(b, h) fp8 quantisation of V (qwen_image_kernel/kv_cache.py:30-45).
+//
+// Both are HBM-bound byte movers: every thread moves one 16-byte chunk of a
+// row (8 elements) per step, rows are read and written whole, and no MFMA is
+// involved.  Floating-point contraction is off in these kernels, so every fp32
+// multiply and add rounds on its own and a plain fp32 restatement reproduces
+// every bit.
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string.h>
+#include <limits.h>
+
+#include "qik_ops.h"
+
+namespace qik_ops {
+
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((__vector_size__(2 * sizeof(__bf16))));
+typedef _Float16 f16x2 __attribute__((__vector_size__(2 * sizeof(_Float16))));
+
+constexpr int NTHREADS = 256;
+
+// two packed 16-bit values <-> fp32
+template <bool FP16>
+__device__ __forceinline__ void unpack2(unsigned w, float& a, float& b) {
+  if constexpr (FP16) {
+    const f16x2 h = __builtin_bit_cast(f16x2, w);
+    a = (float)h[0];
+    b = (float)h[1];
+  } else {
+    a = __uint_as_float(w << 16);
+    b = __uint_as_float(w & 0xffff0000u);
+  }
+}
+template <bool FP16>
+__device__ __forceinline__ unsigned pack2(float a, float b) {  // round to nearest even
+  if constexpr (FP16) {
+    const f16x2 h = {(_Float16)a, (_Float16)b};
+    return __builtin_bit_cast(unsigned, h);
+  } else {
+    const bf16x2 h = {(__bf16)a, (__bf16)b};
+    return __builtin_bit_cast(unsigned, h);
+  }
+}
+// fp32 -> nearest value of the element type -> fp32.  The empty asm pins x as
+// an fp32 value: otherwise the fp16 conversion of a product is folded into
+// v_fma_mixlo_f16, which rounds the exact product once instead of the fp32
+// product (a different result on about one element in 10^4).
+template <bool FP16>
+__device__ __forceinline__ float round_elem(float x) {
+  if constexpr (FP16) {
+    asm volatile("" : "+v"(x));
+    return (float)(_Float16)x;
+  } else {
+    return (float)(__bf16)x;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm + RoPE.  D/8 threads per row, 256/(D/8) rows per workgroup.
+struct RmsRopeParams {
+  const char* x;
+  char* out;
+  const float* w;
+  const float* cos;
+  const float* sin;
+  int64_t rows;  // B*S*H
+  int64_t S, H;
+  int64_t sx[3], so[3];
+  float eps;
+};
+
+template <int D, bool FP16>
+__global__ void __launch_bounds__(NTHREADS) rms_rope_kernel(const RmsRopeParams p) {
+#pragma clang fp contract(off)
+  constexpr int TPR = D / 8;             // threads per row
+  constexpr int RPB = NTHREADS / TPR;    // rows per workgroup
+  constexpr int HALF = D / 2;
+  const int t = threadIdx.x % TPR;       // 16-byte chunk of the row: elements 8t .. 8t+7
+  const int64_t row = (int64_t)blockIdx.x * RPB + threadIdx.x / TPR;
+  const bool live = row < p.rows;
+  const int64_t h = live ? row % p.H : 0;
+  const int64_t bs = live ? row / p.H : 0;
+  const int64_t s = bs % p.S;
+  const int64_t b = bs / p.S;
+
+  u32x4 raw = {0u, 0u, 0u, 0u};
+  if (live) raw = *reinterpret_cast<const u32x4*>(p.x + (b * p.sx[0] + s * p.sx[1] + h * p.sx[2]) * 2 + t * 16);
+  float x[8];
+  unpack2<FP16>(raw.x, x[0], x[1]);
+  unpack2<FP16>(raw.y, x[2], x[3]);
+  unpack2<FP16>(raw.z, x[4], x[5]);
+  unpack2<FP16>(raw.w, x[6], x[7]);
+
+  // sum of squares: the squares of 16-bit inputs are exact in fp32, so only
+  // the additions round; in-thread left to right, then a butterfly over the
+  // row's TPR lanes (lane t adds lane t^k for k = TPR/2 .. 1)
+  float ss = x[0] * x[0];
+#pragma unroll
+  for (int i = 1; i < 8; ++i) ss = ss + x[i] * x[i];
+#pragma unroll
+  for (int k = TPR / 2; k >= 1; k >>= 1) ss = ss + __shfl_xor(ss, k);
+
+  // r = 1 / sqrt(sum / D + eps): the mean is exact (D a power of two), the
+  // sum with eps rounds in fp32, the square root and the reciprocal are taken
+  // in fp64 (both correctly rounded) and rounded once to fp32
+  const float ms = ss * (1.0f / (float)D);
+  const float r = (float)(1.0 / sqrt((double)(ms + p.eps)));
+
+  // n = round((x * r) * w) to the element type, back in fp32 (triton_fused.py:57-58)
+  const float4 w0 = *reinterpret_cast<const float4*>(p.w + 8 * t);
+  const float4 w1 = *reinterpret_cast<const float4*>(p.w + 8 * t + 4);
+  const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+  float n[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) n[i] = round_elem<FP16>((x[i] * r) * wv[i]);
+
+  // pairs (n[2i], n[2i+1]) use frequency 4t + i of position s (:60-66)
+  const float4 c4 = *reinterpret_cast<const float4*>(p.cos + s * HALF + 4 * t);
+  const float4 s4 = *reinterpret_cast<const float4*>(p.sin + s * HALF + 4 * t);
+  const float cs[4] = {c4.x, c4.y, c4.z, c4.w};
+  const float sn[4] = {s4.x, s4.y, s4.z, s4.w};
+  unsigned o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float e = n[2 * i], od = n[2 * i + 1];
+    const float re = e * cs[i] - od * sn[i];
+    const float im = e * sn[i] + od * cs[i];
+    o[i] = pack2<FP16>(re, im);
+  }
+  if (live)
+    *reinterpret_cast<u32x4*>(p.out + (b * p.so[0] + s * p.so[1] + h * p.so[2]) * 2 + t * 16) =
+        u32x4{o[0], o[1], o[2], o[3]};
+}
+
+// ---------------------------------------------------------------------------
+// Slab store.  Row copy [B, P, H, D] -> [B, H, P_max, D] (K, and V unless
+// fp8): threads walk destination rows in order, so each head's block of the
+// slab is written densely; blockIdx.y picks K (0) or V (1).
+struct CopyParams {
+  const char* src[2];
+  char* dst[2];
+  int64_t ss[2][3];  // source b, p, h (elements)
+  int64_t sd[2][3];  // destination b, h, p (elements)
+  int64_t rows;      // B*H*P
+  int64_t P, H;
+  int row_bytes;     // D * element size
+};
+
+__global__ void __launch_bounds__(NTHREADS) slab_copy_kernel(const CopyParams p) {
+  const int which = blockIdx.y;
+  const int tpr = p.row_bytes / 16;
+  const int64_t g = (int64_t)blockIdx.x * NTHREADS + threadIdx.x;
+  const int64_t row = g / tpr;
+  const int t = (int)(g % tpr);
+  if (row >= p.rows) return;
+  const int64_t pp = row % p.P;  // destination row order: b, h, p
+  const int64_t bh = row / p.P;
+  const int64_t h = bh % p.H;
+  const int64_t b = bh / p.H;
+  const u32x4 v = *reinterpret_cast<const u32x4*>(
+      p.src[which] + (b * p.ss[which][0] + pp * p.ss[which][1] + h * p.ss[which][2]) * 2 + t * 16);
+  *reinterpret_cast<u32x4*>(p.dst[which] + (b * p.sd[which][0] + h * p.sd[which][1] + pp * p.sd[which][2]) * 2 +
+                            t * 16) = v;
+}
+
+// fp8 V: one workgroup per (b, h).  Pass 1: amax over the head's P x D values;
+// pass 2 (re-reading the head, now from L2): codes and the scale.
+struct QuantParams {
+  const char* v;     // bf16 [B, P, H, D]
+  char* dst;         // fp8 slab V of the layer
+  float* scale;      // [B*H]
+  int64_t sv[3];     // b, p, h (elements)
+  int64_t sd[3];     // b, h, p (elements = bytes)
+  int64_t P, H;
+};
+
+template <int D>
+__global__ void __launch_bounds__(NTHREADS) slab_quant_fp8_kernel(const QuantParams p) {
+#pragma clang fp contract(off)
+  constexpr int TPR = D / 8;            // threads per row
+  constexpr int RPS = NTHREADS / TPR;   // rows per step
+  __shared__ float red[NTHREADS / 64];
+  const int64_t bh = blockIdx.x;
+  const int64_t h = bh % p.H;
+  const int64_t b = bh / p.H;
+  const int t = threadIdx.x % TPR;
+  const int r0 = threadIdx.x / TPR;
+  const char* src = p.v + (b * p.sv[0] + h * p.sv[2]) * 2 + t * 16;
+
+  float amax = 0.0f;
+  for (int64_t pp = r0; pp < p.P; pp += RPS) {
+    const u32x4 raw = *reinterpret_cast<const u32x4*>(src + pp * p.sv[1] * 2);
+    const unsigned w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      amax = fmaxf(amax, fabsf(__uint_as_float(w[i] << 16)));
+      amax = fmaxf(amax, fabsf(__uint_as_float(w[i] & 0xffff0000u)));
+    }
+  }
+#pragma unroll
+  for (int k = 32; k >= 1; k >>= 1) amax = fmaxf(amax, __shfl_xor(amax, k));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+  __syncthreads();
+  amax = red[0];
+#pragma unroll
+  for (int i = 1; i < NTHREADS / 64; ++i) amax = fmaxf(amax, red[i]);
+
+  // torch: amax / 448.0 multiplies by the fp32 reciprocal; clamp_min(1e-12)
+  const float scale = fmaxf(amax * (1.0f / 448.0f), 1e-12f);
+  if (threadIdx.x == 0) p.scale[bh] = scale;
+
+  char* dst = p.dst + b * p.sd[0] + h * p.sd[1] + t * 8;
+  for (int64_t pp = r0; pp < p.P; pp += RPS) {
+    const u32x4 raw = *reinterpret_cast<const u32x4*>(src + pp * p.sv[1] * 2);
+    const unsigned w[4] = {raw.x, raw.y, raw.z, raw.w};
+    // v / scale (IEEE division), clamped to the e4m3fn range, rounded to
+    // nearest even by the hardware conversion; byte k of the 8 = element 8t+k
+    float q[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      q[2 * i] = fminf(fmaxf(__uint_as_float(w[i] << 16) / scale, -448.0f), 448.0f);
+      q[2 * i + 1] = fminf(fmaxf(__uint_as_float(w[i] & 0xffff0000u) / scale, -448.0f), 448.0f);
+    }
+    int lo = __builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
+    lo = __builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], lo, true);
+    int hi = __builtin_amdgcn_cvt_pk_fp8_f32(q[4], q[5], 0, false);
+    hi = __builtin_amdgcn_cvt_pk_fp8_f32(q[6], q[7], hi, true);
+    *reinterpret_cast<u32x2*>(dst + pp * p.sd[2]) = u32x2{(unsigned)lo, (unsigned)hi};
+  }
+}
+
+inline bool aligned_to(const void* ptr, uintptr_t a) { return (reinterpret_cast<uintptr_t>(ptr) % a) == 0; }
+
+inline bool strides_ok(const int64_t st[3], int64_t mult) {
+  return st[0] % mult == 0 && st[1] % mult == 0 && st[2] % mult == 0;
+}
+
+inline bool sizes_ok(int64_t a, int64_t b, int64_t c, int64_t d) {
+  if (a < 0 || b < 0 || c < 0 || d < 0) return false;
+  const int64_t lim = (int64_t)INT_MAX;
+  return a <= lim && b <= lim && c <= lim && (a == 0 || b == 0 || c == 0 || a * b * c <= lim * 64);
+}
+
+}  // namespace qik_ops
+
+extern "C" {
+
+int qik_rms_rope(const qik_rms_rope_args* a, void* stream) {
+  using namespace qik_ops;
+  if (a == nullptr) return QIK_ERR_NULL_ARG;
+  if (a->abi_version != QIK_ABI_VERSION || a->reserved0 != 0) return QIK_ERR_ABI_VERSION;
+  if (a->dtype != QIK_DTYPE_BF16 && a->dtype != QIK_DTYPE_FP16) return QIK_ERR_DTYPE;
+  if (a->D != 64 && a->D != 128) return QIK_ERR_HEAD_DIM;
+  if (!sizes_ok(a->B, a->S, a->H, a->D)) return QIK_ERR_SHAPE;
+  const int64_t rows = a->B * a->S * a->H;
+  if (rows == 0) return QIK_OK;
+  if (a->x == nullptr || a->out == nullptr || a->weight == nullptr || a->cos == nullptr || a->sin == nullptr)
+    return QIK_ERR_NULL_ARG;
+  if (!aligned_to(a->x, 16) || !aligned_to(a->out, 16) || !aligned_to(a->weight, 16) || !aligned_to(a->cos, 16) ||
+      !aligned_to(a->sin, 16))
+    return QIK_ERR_ALIGN;
+  if (!strides_ok(a->stride_x, 8) || !strides_ok(a->stride_out, 8)) return QIK_ERR_ALIGN;
+
+  RmsRopeParams p;
+  memset(&p, 0, sizeof(p));
+  p.x = static_cast<const char*>(a->x);
+  p.out = static_cast<char*>(a->out);
+  p.w = a->weight;
+  p.cos = a->cos;
+  p.sin = a->sin;
+  p.rows = rows;
+  p.S = a->S;
+  p.H = a->H;
+  for (int i = 0; i < 3; ++i) {
+    p.sx[i] = a->stride_x[i];
+    p.so[i] = a->stride_out[i];
+  }
+  p.eps = a->eps;
+  const bool fp16 = a->dtype == QIK_DTYPE_FP16;
+  const int rpb = NTHREADS / (int)(a->D / 8);
+  const int64_t grid = (rows + rpb - 1) / rpb;
+  if (grid > (int64_t)UINT_MAX) return QIK_ERR_SHAPE;
+  const void* fn;
+  if (a->D == 128) fn = fp16 ? (const void*)rms_rope_kernel<128, true> : (const void*)rms_rope_kernel<128, false>;
+  else fn = fp16 ? (const void*)rms_rope_kernel<64, true> : (const void*)rms_rope_kernel<64, false>;
+  void* kargs[] = {&p};
+  const hipError_t e =
+      hipLaunchKernel(fn, dim3((unsigned)grid), dim3(NTHREADS), kargs, 0, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? QIK_OK : QIK_ERR_LAUNCH;
+}
+
+int qik_slab_store(const qik_slab_store_args* a, void* stream) {
+  using namespace qik_ops;
+  if (a == nullptr) return QIK_ERR_NULL_ARG;
+  if (a->abi_version != QIK_ABI_VERSION || a->reserved0 != 0) return QIK_ERR_ABI_VERSION;
+  if (a->dtype != QIK_DTYPE_BF16 && a->dtype != QIK_DTYPE_FP16) return QIK_ERR_DTYPE;
+  const bool fp8 = a->v_fp8 != 0;
+  if (fp8 && a->dtype != QIK_DTYPE_BF16) return QIK_ERR_FP8_SCALE;
+  if (fp8 != (a->v_scale != nullptr)) return QIK_ERR_FP8_SCALE;
+  if (a->D != 64 && a->D != 128) return QIK_ERR_HEAD_DIM;
+  if (!sizes_ok(a->B, a->P, a->H, a->D)) return QIK_ERR_SHAPE;
+  const int64_t rows = a->B * a->H * a->P;
+  if (rows == 0) return QIK_OK;
+  if (a->k == nullptr || a->v == nullptr || a->k_dst == nullptr || a->v_dst == nullptr) return QIK_ERR_NULL_ARG;
+  if (!aligned_to(a->k, 16) || !aligned_to(a->v, 16) || !aligned_to(a->k_dst, 16)) return QIK_ERR_ALIGN;
+  if (!aligned_to(a->v_dst, fp8 ? 8 : 16)) return QIK_ERR_ALIGN;
+  if (!strides_ok(a->stride_k, 8) || !strides_ok(a->stride_v, 8) || !strides_ok(a->stride_k_dst, 8) ||
+      !strides_ok(a->stride_v_dst, 8))
+    return QIK_ERR_ALIGN;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+
+  CopyParams cp;
+  memset(&cp, 0, sizeof(cp));
+  cp.src[0] = static_cast<const char*>(a->k);
+  cp.dst[0] = static_cast<char*>(a->k_dst);
+  cp.src[1] = static_cast<const char*>(a->v);
+  cp.dst[1] = static_cast<char*>(a->v_dst);
+  for (int i = 0; i < 3; ++i) {
+    cp.ss[0][i] = a->stride_k[i];
+    cp.sd[0][i] = a->stride_k_dst[i];
+    cp.ss[1][i] = a->stride_v[i];
+    cp.sd[1][i] = a->stride_v_dst[i];
+  }
+  cp.rows = rows;
+  cp.P = a->P;
+  cp.H = a->H;
+  cp.row_bytes = (int)(a->D * 2);
+  const int64_t threads = rows * (a->D * 2 / 16);
+  const int64_t grid = (threads + NTHREADS - 1) / NTHREADS;
+  if (grid > (int64_t)UINT_MAX || a->B * a->H > (int64_t)UINT_MAX) return QIK_ERR_SHAPE;
+  void* cargs[] = {&cp};
+  hipError_t e = hipLaunchKernel(reinterpret_cast<const void*>(slab_copy_kernel), dim3((unsigned)grid, fp8 ? 1 : 2),
+                                 dim3(NTHREADS), cargs, 0, s);
+  if (e != hipSuccess) return QIK_ERR_LAUNCH;
+  if (!fp8) return QIK_OK;
+
+  QuantParams qp;
+  memset(&qp, 0, sizeof(qp));
+  qp.v = static_cast<const char*>(a->v);
+  qp.dst = static_cast<char*>(a->v_dst);
+  qp.scale = a->v_scale;
+  for (int i = 0; i < 3; ++i) {
+    qp.sv[i] = a->stride_v[i];
+    qp.sd[i] = a->stride_v_dst[i];
+  }
+  qp.P = a->P;
+  qp.H = a->H;
+  const void* fn = a->D == 128 ? (const void*)slab_quant_fp8_kernel<128> : (const void*)slab_quant_fp8_kernel<64>;
+  void* qargs[] = {&qp};
+  e = hipLaunchKernel(fn, dim3((unsigned)(a->B * a->H)), dim3(NTHREADS), qargs, 0, s);
+  return e == hipSuccess ? QIK_OK : QIK_ERR_LAUNCH;
+}
+
+}  // extern "C"

@@ -8,6 +8,12 @@ head's prefix tokens are dense (256 B rows of bf16 K, 128 B rows of fp8 V), and
 ``views()`` returns ``[B, P, H, D]`` strided views that the attention kernel
 reads in place.
 
+``store`` on a HIP device is one call of ``qik_slab_store`` (include/qik_ops.h):
+the transposed copy of K (and of a bf16 V) and, for an fp8 slab, the per-(b, h)
+amax, scale and e4m3fn codes of V, bit-identical to the torch ops of
+kv_cache.py:36-42 run on the same device.  A slab on the CPU (the reference's
+own CPU-runnable case) runs those torch ops.
+
 Difference from the reference: the prefix length of each layer is also kept on
 the host, so ``get()``/``views()`` do not synchronise the device
 (the reference reads ``int(lengths[layer])``, kv_cache.py:49, 56).
@@ -15,7 +21,11 @@ the host, so ``get()``/``views()`` do not synchronise the device
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
+
+from . import _lib
 
 FP8_E4M3_MAX = 448.0
 
@@ -38,6 +48,47 @@ class _LayerView:
         P = k.shape[1]
         if P > c.capacity:
             raise ValueError(f"prefix of {P} tokens exceeds the slab capacity {c.capacity}")
+        if c.k_buf.is_cuda:
+            self._store_device(k, v, P)
+        else:
+            self._store_torch(k, v, P)
+        c.lengths[self._layer] = P
+        c._host_lengths[self._layer] = P
+
+    def _store_device(self, k: torch.Tensor, v: torch.Tensor, P: int) -> None:
+        c = self._c
+        if k.shape != v.shape or k.dim() != 4 or tuple(k.shape[2:]) != tuple(c.k_buf.shape[2:3] + c.k_buf.shape[4:]):
+            raise ValueError(f"k, v must be [B, P, H, D] matching the slab, got {tuple(k.shape)}, {tuple(v.shape)}")
+        if k.shape[0] != c.batch_size:
+            raise ValueError(f"batch {k.shape[0]} != slab batch {c.batch_size}")
+        k = k.to(device=c.k_buf.device, dtype=c.k_buf.dtype)
+        v = v.to(device=c.k_buf.device, dtype=c.k_buf.dtype)
+        if k.stride(-1) != 1:
+            k = k.contiguous()
+        if v.stride(-1) != 1:
+            v = v.contiguous()
+        kd = c.k_buf[self._layer]
+        vd = c.v_buf[self._layer]
+        a = _lib.QikSlabStoreArgs()
+        a.abi_version = _lib.ABI_VERSION
+        a.dtype = _lib.DTYPE_BF16 if c.k_buf.dtype == torch.bfloat16 else _lib.DTYPE_FP16
+        a.v_fp8 = 1 if c.v_fp8 else 0
+        a.k = k.data_ptr()
+        a.v = v.data_ptr()
+        a.k_dst = kd.data_ptr()
+        a.v_dst = vd.data_ptr()
+        a.v_scale = c.v_scale[self._layer].data_ptr() if c.v_fp8 else None
+        a.B, a.P, a.H, a.D = k.shape[0], P, k.shape[2], k.shape[3]
+        a.stride_k = _lib._i64x3(k.stride(0), k.stride(1), k.stride(2))
+        a.stride_v = _lib._i64x3(v.stride(0), v.stride(1), v.stride(2))
+        a.stride_k_dst = _lib._i64x3(kd.stride(0), kd.stride(1), kd.stride(2))
+        a.stride_v_dst = _lib._i64x3(vd.stride(0), vd.stride(1), vd.stride(2))
+        with torch.cuda.device(kd.device):
+            stream = torch.cuda.current_stream(kd.device).cuda_stream
+            _lib.check(_lib.load().qik_slab_store(ctypes.byref(a), stream), "qik_slab_store")
+
+    def _store_torch(self, k: torch.Tensor, v: torch.Tensor, P: int) -> None:
+        c = self._c
         c.k_buf[self._layer, :, :, :P, :].copy_(k.transpose(1, 2))
         if c.v_fp8:
             vt = v.transpose(1, 2).float()
@@ -48,8 +99,6 @@ class _LayerView:
             c.v_scale[self._layer].copy_(scale)
         else:
             c.v_buf[self._layer, :, :, :P, :].copy_(v.transpose(1, 2))
-        c.lengths[self._layer] = P
-        c._host_lengths[self._layer] = P
 
     def get(self):
         """(k, v) as [B, P, H, D] strided views."""

@@ -20,11 +20,14 @@ from qwen_image_kernel_amd import _lib, attention
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "qik_attn.h")
+HEADERS = [HEADER, os.path.join(ROOT, "include", "qik_ops.h")]
 
 
 def header_functions():
-    text = open(HEADER).read()
-    return sorted(set(re.findall(r"^[A-Za-z_][\w\s\*]*?\b(qik_\w+)\s*\(", text, flags=re.M)))
+    names = set()
+    for h in HEADERS:
+        names |= set(re.findall(r"^[A-Za-z_][\w\s\*]*?\b(qik_\w+)\s*\(", open(h).read(), flags=re.M))
+    return sorted(names)
 
 
 def test_library_loads_and_exports_every_declared_symbol():
@@ -37,12 +40,15 @@ def test_library_loads_and_exports_every_declared_symbol():
     assert lib.qik_abi_version() == _lib.ABI_VERSION
 
 
-def test_struct_layout_matches_c_header(tmp_path):
-    fields = [f for f, _ in _lib.QikAttnArgs._fields_]
-    src = ["#include <stdio.h>", "#include <stddef.h>", '#include "qik_attn.h"', "int main(void) {",
-           'printf("sizeof %zu\\n", sizeof(qik_attn_args));']
+@pytest.mark.parametrize("cname,pytype", [("qik_attn_args", _lib.QikAttnArgs),
+                                           ("qik_rms_rope_args", _lib.QikRmsRopeArgs),
+                                           ("qik_slab_store_args", _lib.QikSlabStoreArgs)])
+def test_struct_layout_matches_c_header(tmp_path, cname, pytype):
+    fields = [f for f, _ in pytype._fields_]
+    src = ["#include <stdio.h>", "#include <stddef.h>", '#include "qik_ops.h"', "int main(void) {",
+           f'printf("sizeof %zu\\n", sizeof({cname}));']
     for f in fields:
-        src.append(f'printf("{f} %zu\\n", offsetof(qik_attn_args, {f}));')
+        src.append(f'printf("{f} %zu\\n", offsetof({cname}, {f}));')
     src.append("return 0; }")
     c = tmp_path / "layout.c"
     c.write_text("\n".join(src))
@@ -50,9 +56,9 @@ def test_struct_layout_matches_c_header(tmp_path):
     subprocess.run(["gcc", "-std=c99", f"-I{os.path.dirname(HEADER)}", str(c), "-o", str(exe)], check=True)
     got = dict(line.split() for line in subprocess.run([str(exe)], capture_output=True, text=True,
                                                         check=True).stdout.splitlines())
-    assert int(got["sizeof"]) == ctypes.sizeof(_lib.QikAttnArgs)
+    assert int(got["sizeof"]) == ctypes.sizeof(pytype)
     for f in fields:
-        assert int(got[f]) == getattr(_lib.QikAttnArgs, f).offset, f
+        assert int(got[f]) == getattr(pytype, f).offset, f
 
 
 def _valid_args(**kw):
@@ -176,3 +182,58 @@ def test_wrapper_keeps_reference_asserts_on_cpu():
     with pytest.raises(AssertionError):
         attention.block_causal_flash_attention(qb, qb, qb, torch.zeros(8, dtype=torch.int32), None,
                                                cache_k=ck, cache_v=ck)
+
+
+def _rope_args(**kw):
+    a = _lib.QikRmsRopeArgs()
+    a.abi_version = _lib.ABI_VERSION
+    a.dtype = _lib.DTYPE_BF16
+    a.B, a.S, a.H, a.D = 1, 16, 2, 128
+    a.x = a.out = a.weight = a.cos = a.sin = 0x10000
+    a.stride_x = a.stride_out = _lib._i64x3(16 * 2 * 128, 2 * 128, 128)
+    a.eps = 1e-6
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(abi_version=3), -2), (dict(reserved0=1), -2), (dict(dtype=5), -3), (dict(D=96), -4),
+    (dict(S=-2), -5), (dict(x=None), -1), (dict(cos=None), -1), (dict(out=0x10004), -8),
+    (dict(stride_x=_lib._i64x3(4096, 260, 128)), -8),
+])
+def test_rms_rope_rejects_before_any_device_call(kw, code):
+    assert _lib.load().qik_rms_rope(ctypes.byref(_rope_args(**kw)), None) == code
+
+
+def test_rms_rope_without_rows_is_a_no_op():
+    assert _lib.load().qik_rms_rope(ctypes.byref(_rope_args(S=0, x=None)), None) == 0
+
+
+def _store_args(**kw):
+    a = _lib.QikSlabStoreArgs()
+    a.abi_version = _lib.ABI_VERSION
+    a.dtype = _lib.DTYPE_BF16
+    a.v_fp8 = 1
+    a.k = a.v = a.k_dst = a.v_dst = a.v_scale = 0x10000
+    a.B, a.P, a.H, a.D = 1, 32, 2, 128
+    a.stride_k = a.stride_v = _lib._i64x3(32 * 2 * 128, 2 * 128, 128)
+    a.stride_k_dst = a.stride_v_dst = _lib._i64x3(2 * 48 * 128, 48 * 128, 128)
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(abi_version=0), -2), (dict(dtype=9), -3), (dict(D=32), -4), (dict(P=-1), -5),
+    (dict(v_scale=None), -7),                     # fp8 V needs the scale output
+    (dict(v_fp8=0), -7),                          # a scale output without fp8 V
+    (dict(dtype=_lib.DTYPE_FP16), -7),            # fp8 V only from bf16 (triton_attention.py:159)
+    (dict(k=None), -1), (dict(v_dst=0x10004), -8), (dict(stride_k=_lib._i64x3(8192, 260, 128)), -8),
+])
+def test_slab_store_rejects_before_any_device_call(kw, code):
+    assert _lib.load().qik_slab_store(ctypes.byref(_store_args(**kw)), None) == code
+
+
+def test_slab_store_without_rows_is_a_no_op():
+    assert _lib.load().qik_slab_store(ctypes.byref(_store_args(P=0, k=None)), None) == 0
