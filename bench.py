@@ -12,6 +12,14 @@ counts 2*D for QK^T and 2*D for PV per allowed (query, key) pair.
 
 Prints ONE JSON line (rank 0, N=1).  ``--gpus N`` with N > 1 exits with a
 message: this build runs on one GPU.
+
+``side_ops`` in the same line (outside the timed step, not part of ``value``):
+the two HBM-bound kernels beside the attention call, each at its shape in the
+headline workloads -- per-head RMSNorm + RoPE of the 1024px Q ([1, 4352, 24,
+128] bf16) and the slab store of the 768px edit prefix ([1, 2560, 24, 128] K
+and V, V to fp8) -- device time per call of prebuilt C-ABI launches back to back (``us``), the
+time per call through the Python API (``api_us``), priced in algorithmic HBM
+bytes against 8 TB/s, beside the same torch computation on the host CPU.
 """
 
 from __future__ import annotations
@@ -136,6 +144,112 @@ def cpu_baseline(wls, budget_s: float) -> dict:
     }
 
 
+def _event_us(fn, reps: int) -> float:
+    """Average device time of fn() in microseconds (HIP events on the current stream)."""
+    import torch
+
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        fn()
+        e1.record()
+        ts.append((e0, e1))
+    torch.cuda.synchronize()
+    return sum(a.elapsed_time(b) for a, b in ts) / reps * 1e3
+
+
+def _batch_us(fn, reps: int) -> float:
+    """Device time per call of fn() launched back to back (two events around the batch)."""
+    import torch
+
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps * 1e3
+
+
+def _cpu_us(fn, reps: int) -> float:
+    fn()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        fn()
+    return (time.perf_counter() - t0) / reps * 1e6
+
+
+def side_ops(qik, wls, dev, with_cpu: bool) -> dict:
+    """RMSNorm + RoPE of the 1024px Q and the slab store of the 768px edit prefix."""
+    import torch
+
+    out = {}
+    g = torch.Generator(device="cuda").manual_seed(77)
+    t2i = wls.workload("t2i_1024")
+    B, S, H, D = t2i.B, t2i.SQ, t2i.H, t2i.D
+    x = torch.randn(B, S, H, D, generator=g, device=dev).to(torch.bfloat16)
+    w = torch.randn(D, generator=g, device=dev) * 0.3 + 1.0
+    inv = 1.0 / (10000 ** (torch.arange(0, D, 2, device=dev).float() / D))
+    ang = torch.outer(torch.arange(S, device=dev).float(), inv)
+    freqs = torch.polar(torch.ones_like(ang), ang)
+    import ctypes
+
+    from qwen_image_kernel_amd import _lib, fused
+
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    cos, sin = freqs.real.float().contiguous(), freqs.imag.float().contiguous()
+    y = torch.empty_like(x)
+    ra = fused.rms_rope_args(x, w, cos, sin, y, 1e-6)
+    us = _batch_us(lambda: lib.qik_rms_rope(ctypes.byref(ra), stream), 50)
+    api_us = _event_us(lambda: qik.fused_rms_norm_rope(x, w, freqs, 1e-6), 20)
+    nbytes = 2 * B * S * H * D * 2 + D * 4 + S * (D // 2) * 8   # x in, out, weight, cos/sin
+    entry = {"shape": [B, S, H, D], "kernel": "rms_rope_kernel<128,bf16>", "us": round(us, 2),
+             "api_us": round(api_us, 2),
+             "algorithmic_bytes": nbytes, "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+             "frac_hbm": round(nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4)}
+    if with_cpu:
+        xc, wc, fc = x.cpu(), w.cpu(), freqs.cpu()
+
+        def stock():  # the stock composition (tests/test_fused.py:21-33) in torch on the CPU
+            var = xc.float().pow(2).mean(-1, keepdim=True)
+            y = (xc * torch.rsqrt(var + 1e-6) * wc).to(xc.dtype)
+            r = torch.view_as_complex(y.float().reshape(B, S, H, -1, 2)) * fc.unsqueeze(1)
+            return torch.view_as_real(r).flatten(-2).to(xc.dtype)
+        entry["cpu_torch_us"] = round(_cpu_us(stock, 3), 1)
+        entry["cpu_threads"] = torch.get_num_threads()
+    out["rms_rope_t2i_1024_q"] = entry
+
+    ed = wls.workload("edit_768")
+    B, P, H, D = ed.B, ed.P, ed.H, ed.D
+    k = torch.randn(B, P, H, D, generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn(B, P, H, D, generator=g, device=dev).to(torch.bfloat16)
+    cache = qik.ContiguousKVCache(1, B, P + 272, H, D, v_fp8=True, device=dev)
+    layer = cache.get_layer(0)
+    sa, keep = layer.store_args(k, v, P)
+    us = _batch_us(lambda: lib.qik_slab_store(ctypes.byref(sa), stream), 50)
+    api_us = _event_us(lambda: layer.store(k, v), 20)
+    nbytes = B * P * H * D * (2 + 2 + 2 + 1) + B * H * 4   # k, v in; k bf16, v fp8 out; scales
+    entry = {"shape": [B, P, H, D],
+             "kernels": "slab_copy_kernel + slab_scale_fp8_kernel<128> + slab_quant_fp8_kernel<128>",
+             "us": round(us, 2), "api_us": round(api_us, 2), "algorithmic_bytes": nbytes,
+             "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+             "frac_hbm": round(nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4)}
+    if with_cpu:
+        kc, vc = k.cpu(), v.cpu()
+        ccache = qik.ContiguousKVCache(1, B, P + 272, H, D, v_fp8=True, device="cpu")
+        entry["cpu_torch_us"] = round(_cpu_us(lambda: ccache.get_layer(0).store(kc, vc), 3), 1)
+    out["slab_store_edit_768_prefix"] = entry
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -226,6 +340,9 @@ def main():
     dwl = wls.workload(dom)
     achieved = dwl.flops() / (per_workload[dom]["kernel_avg_us"] * 1e-6) / 1e12
 
+    del layers, calls
+    sops = side_ops(qik, wls, dev, with_cpu=args.cpu_seconds > 0)
+
     cpu = None
     if args.cpu_seconds > 0:
         cpu = cpu_baseline(wls, args.cpu_seconds)
@@ -263,6 +380,7 @@ def main():
             "compulsory_bytes_per_launch": dwl.min_bytes(),
         },
         "per_workload": per_workload,
+        "side_ops": sops,
         "cpu_baseline": cpu,
         "wall_s_timed": round(wall, 3),
     }

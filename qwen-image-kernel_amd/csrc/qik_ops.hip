@@ -13,6 +13,7 @@
 #include <stdint.h>
 #include <string.h>
 #include <limits.h>
+#include <algorithm>
 
 #include "qik_ops.h"
 
@@ -69,28 +70,18 @@ struct RmsRopeParams {
   const float* w;
   const float* cos;
   const float* sin;
-  int64_t rows;  // B*S*H
-  int64_t S, H;
+  int rows;      // B*S*H (< 2^31, checked on the host)
+  int S, H;
   int64_t sx[3], so[3];
   float eps;
 };
 
+// One row: x (8 elements of chunk t already in registers) -> 16 output bytes.
 template <int D, bool FP16>
-__global__ void __launch_bounds__(NTHREADS) rms_rope_kernel(const RmsRopeParams p) {
+__device__ __forceinline__ u32x4 rms_rope_chunk(const u32x4 raw, const int t, const float (&wv)[8],
+                                                const float4 c4, const float4 s4, const float eps) {
 #pragma clang fp contract(off)
-  constexpr int TPR = D / 8;             // threads per row
-  constexpr int RPB = NTHREADS / TPR;    // rows per workgroup
-  constexpr int HALF = D / 2;
-  const int t = threadIdx.x % TPR;       // 16-byte chunk of the row: elements 8t .. 8t+7
-  const int64_t row = (int64_t)blockIdx.x * RPB + threadIdx.x / TPR;
-  const bool live = row < p.rows;
-  const int64_t h = live ? row % p.H : 0;
-  const int64_t bs = live ? row / p.H : 0;
-  const int64_t s = bs % p.S;
-  const int64_t b = bs / p.S;
-
-  u32x4 raw = {0u, 0u, 0u, 0u};
-  if (live) raw = *reinterpret_cast<const u32x4*>(p.x + (b * p.sx[0] + s * p.sx[1] + h * p.sx[2]) * 2 + t * 16);
+  constexpr int TPR = D / 8;
   float x[8];
   unpack2<FP16>(raw.x, x[0], x[1]);
   unpack2<FP16>(raw.y, x[2], x[3]);
@@ -110,19 +101,14 @@ __global__ void __launch_bounds__(NTHREADS) rms_rope_kernel(const RmsRopeParams 
   // sum with eps rounds in fp32, the square root and the reciprocal are taken
   // in fp64 (both correctly rounded) and rounded once to fp32
   const float ms = ss * (1.0f / (float)D);
-  const float r = (float)(1.0 / sqrt((double)(ms + p.eps)));
+  const float r = (float)(1.0 / sqrt((double)(ms + eps)));
 
   // n = round((x * r) * w) to the element type, back in fp32 (triton_fused.py:57-58)
-  const float4 w0 = *reinterpret_cast<const float4*>(p.w + 8 * t);
-  const float4 w1 = *reinterpret_cast<const float4*>(p.w + 8 * t + 4);
-  const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
   float n[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) n[i] = round_elem<FP16>((x[i] * r) * wv[i]);
 
-  // pairs (n[2i], n[2i+1]) use frequency 4t + i of position s (:60-66)
-  const float4 c4 = *reinterpret_cast<const float4*>(p.cos + s * HALF + 4 * t);
-  const float4 s4 = *reinterpret_cast<const float4*>(p.sin + s * HALF + 4 * t);
+  // pairs (n[2i], n[2i+1]) use frequency 4t + i of the row's position (:60-66)
   const float cs[4] = {c4.x, c4.y, c4.z, c4.w};
   const float sn[4] = {s4.x, s4.y, s4.z, s4.w};
   unsigned o[4];
@@ -133,9 +119,50 @@ __global__ void __launch_bounds__(NTHREADS) rms_rope_kernel(const RmsRopeParams 
     const float im = e * sn[i] + od * cs[i];
     o[i] = pack2<FP16>(re, im);
   }
-  if (live)
-    *reinterpret_cast<u32x4*>(p.out + (b * p.so[0] + s * p.so[1] + h * p.so[2]) * 2 + t * 16) =
-        u32x4{o[0], o[1], o[2], o[3]};
+  (void)t;
+  return u32x4{o[0], o[1], o[2], o[3]};
+}
+
+// RR rows per thread, their loads issued before any arithmetic; RPB rows per
+// workgroup pass, RR passes per workgroup.
+constexpr int RR = 4;
+
+template <int D, bool FP16>
+__global__ void __launch_bounds__(NTHREADS) rms_rope_kernel(const RmsRopeParams p) {
+  constexpr int TPR = D / 8;             // threads per row
+  constexpr int RPB = NTHREADS / TPR;    // rows per pass
+  constexpr int HALF = D / 2;
+  const int t = threadIdx.x % TPR;       // 16-byte chunk of the row: elements 8t .. 8t+7
+  const int row0 = blockIdx.x * (RPB * RR) + threadIdx.x / TPR;
+
+  const float4 w0 = *reinterpret_cast<const float4*>(p.w + 8 * t);
+  const float4 w1 = *reinterpret_cast<const float4*>(p.w + 8 * t + 4);
+  const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+
+  u32x4 raw[RR];
+  float4 c4[RR], s4[RR];
+  int64_t ooff[RR];
+  bool live[RR];
+#pragma unroll
+  for (int u = 0; u < RR; ++u) {
+    const int row = row0 + u * RPB;
+    live[u] = row < p.rows;
+    const unsigned bs = live[u] ? (unsigned)row / (unsigned)p.H : 0u;
+    const int h = live[u] ? row - (int)bs * p.H : 0;
+    const int b = (int)(bs / (unsigned)p.S);
+    const int s = (int)bs - b * p.S;
+    raw[u] = u32x4{0u, 0u, 0u, 0u};
+    if (live[u])
+      raw[u] = *reinterpret_cast<const u32x4*>(p.x + (b * p.sx[0] + s * p.sx[1] + h * p.sx[2]) * 2 + t * 16);
+    c4[u] = *reinterpret_cast<const float4*>(p.cos + s * HALF + 4 * t);
+    s4[u] = *reinterpret_cast<const float4*>(p.sin + s * HALF + 4 * t);
+    ooff[u] = (b * p.so[0] + s * p.so[1] + h * p.so[2]) * 2 + t * 16;
+  }
+#pragma unroll
+  for (int u = 0; u < RR; ++u) {
+    const u32x4 o = rms_rope_chunk<D, FP16>(raw[u], t, wv, c4[u], s4[u], p.eps);
+    if (live[u]) *reinterpret_cast<u32x4*>(p.out + ooff[u]) = o;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -145,6 +172,8 @@ __global__ void __launch_bounds__(NTHREADS) rms_rope_kernel(const RmsRopeParams 
 struct CopyParams {
   const char* src[2];
   char* dst[2];
+  float* zero;       // fp8 V: the [B*H] scales, zeroed for the atomic max that follows (else NULL)
+  int64_t nzero;
   int64_t ss[2][3];  // source b, p, h (elements)
   int64_t sd[2][3];  // destination b, h, p (elements)
   int64_t rows;      // B*H*P
@@ -156,6 +185,7 @@ __global__ void __launch_bounds__(NTHREADS) slab_copy_kernel(const CopyParams p)
   const int which = blockIdx.y;
   const int tpr = p.row_bytes / 16;
   const int64_t g = (int64_t)blockIdx.x * NTHREADS + threadIdx.x;
+  if (p.zero != nullptr && which == 0 && g < p.nzero) p.zero[g] = 0.0f;
   const int64_t row = g / tpr;
   const int t = (int)(g % tpr);
   if (row >= p.rows) return;
@@ -169,55 +199,92 @@ __global__ void __launch_bounds__(NTHREADS) slab_copy_kernel(const CopyParams p)
                             t * 16) = v;
 }
 
-// fp8 V: one workgroup per (b, h).  Pass 1: amax over the head's P x D values;
-// pass 2 (re-reading the head, now from L2): codes and the scale.
+// fp8 V in two launches over `chunks` workgroups per (b, h), workgroup c
+// owning rows [c*P/chunks, (c+1)*P/chunks) of the head:
+//   slab_scale_fp8_kernel: scale of its rows, max(amax * fp32(1/448), 1e-12),
+//     atomically maxed into scale[b*H + h] (zeroed by the copy launch before).
+//     The map amax -> scale is monotone (fp32 rounding included), so the max of
+//     the rows' scales is the scale of the head's amax;
+//   slab_quant_fp8_kernel: the codes of its rows with the head's scale.
 struct QuantParams {
   const char* v;     // bf16 [B, P, H, D]
   char* dst;         // fp8 slab V of the layer
   float* scale;      // [B*H]
   int64_t sv[3];     // b, p, h (elements)
   int64_t sd[3];     // b, h, p (elements = bytes)
-  int64_t P, H;
+  int P, H, chunks;
 };
 
+constexpr int QTHREADS = 512;
+
 template <int D>
-__global__ void __launch_bounds__(NTHREADS) slab_quant_fp8_kernel(const QuantParams p) {
-#pragma clang fp contract(off)
-  constexpr int TPR = D / 8;            // threads per row
-  constexpr int RPS = NTHREADS / TPR;   // rows per step
-  __shared__ float red[NTHREADS / 64];
-  const int64_t bh = blockIdx.x;
-  const int64_t h = bh % p.H;
-  const int64_t b = bh / p.H;
+__global__ void __launch_bounds__(QTHREADS) slab_scale_fp8_kernel(const QuantParams p) {
+  constexpr int TPR = D / 8;             // threads per row
+  constexpr int RPS = QTHREADS / TPR;    // rows per step
+  constexpr int U = 4;                   // steps in flight per thread
+  __shared__ float red[QTHREADS / 64];
+  const int bh = blockIdx.x / p.chunks;
+  const int c = blockIdx.x - bh * p.chunks;
+  const int h = bh % p.H;
+  const int b = bh / p.H;
   const int t = threadIdx.x % TPR;
   const int r0 = threadIdx.x / TPR;
   const char* src = p.v + (b * p.sv[0] + h * p.sv[2]) * 2 + t * 16;
+  const int64_t rs = p.sv[1] * 2;        // source row stride, bytes
+  const int p0 = (int)((int64_t)p.P * c / p.chunks);
+  const int p1 = (int)((int64_t)p.P * (c + 1) / p.chunks);
 
   float amax = 0.0f;
-  for (int64_t pp = r0; pp < p.P; pp += RPS) {
-    const u32x4 raw = *reinterpret_cast<const u32x4*>(src + pp * p.sv[1] * 2);
+  auto absmax8 = [&](const u32x4 raw) __attribute__((always_inline)) {
     const unsigned w[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       amax = fmaxf(amax, fabsf(__uint_as_float(w[i] << 16)));
       amax = fmaxf(amax, fabsf(__uint_as_float(w[i] & 0xffff0000u)));
     }
+  };
+  int pp = p0 + r0;
+  for (; pp + (U - 1) * RPS < p1; pp += U * RPS) {
+    u32x4 raw[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) raw[u] = *reinterpret_cast<const u32x4*>(src + (pp + u * RPS) * rs);
+#pragma unroll
+    for (int u = 0; u < U; ++u) absmax8(raw[u]);
   }
+  for (; pp < p1; pp += RPS) absmax8(*reinterpret_cast<const u32x4*>(src + pp * rs));
 #pragma unroll
   for (int k = 32; k >= 1; k >>= 1) amax = fmaxf(amax, __shfl_xor(amax, k));
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
   __syncthreads();
-  amax = red[0];
-#pragma unroll
-  for (int i = 1; i < NTHREADS / 64; ++i) amax = fmaxf(amax, red[i]);
+  if (threadIdx.x == 0) {
+    for (int i = 1; i < QTHREADS / 64; ++i) amax = fmaxf(amax, red[i]);
+    amax = fmaxf(amax, red[0]);
+    // torch: amax / 448.0 multiplies by the fp32 reciprocal; clamp_min(1e-12).
+    // Non-negative fp32 values order like their bit patterns.
+    const float sc = fmaxf(amax * (1.0f / 448.0f), 1e-12f);
+    atomicMax(reinterpret_cast<unsigned*>(p.scale) + bh, __float_as_uint(sc));
+  }
+}
 
-  // torch: amax / 448.0 multiplies by the fp32 reciprocal; clamp_min(1e-12)
-  const float scale = fmaxf(amax * (1.0f / 448.0f), 1e-12f);
-  if (threadIdx.x == 0) p.scale[bh] = scale;
-
+template <int D>
+__global__ void __launch_bounds__(QTHREADS) slab_quant_fp8_kernel(const QuantParams p) {
+#pragma clang fp contract(off)
+  constexpr int TPR = D / 8;             // threads per row
+  constexpr int RPS = QTHREADS / TPR;    // rows per step
+  const int bh = blockIdx.x / p.chunks;
+  const int c = blockIdx.x - bh * p.chunks;
+  const int h = bh % p.H;
+  const int b = bh / p.H;
+  const int t = threadIdx.x % TPR;
+  const int r0 = threadIdx.x / TPR;
+  const char* src = p.v + (b * p.sv[0] + h * p.sv[2]) * 2 + t * 16;
+  const int64_t rs = p.sv[1] * 2;
+  const int p0 = (int)((int64_t)p.P * c / p.chunks);
+  const int p1 = (int)((int64_t)p.P * (c + 1) / p.chunks);
+  const float scale = p.scale[bh];
   char* dst = p.dst + b * p.sd[0] + h * p.sd[1] + t * 8;
-  for (int64_t pp = r0; pp < p.P; pp += RPS) {
-    const u32x4 raw = *reinterpret_cast<const u32x4*>(src + pp * p.sv[1] * 2);
+  for (int q0 = p0 + r0; q0 < p1; q0 += RPS) {
+    const u32x4 raw = *reinterpret_cast<const u32x4*>(src + q0 * rs);
     const unsigned w[4] = {raw.x, raw.y, raw.z, raw.w};
     // v / scale (IEEE division), clamped to the e4m3fn range, rounded to
     // nearest even by the hardware conversion; byte k of the 8 = element 8t+k
@@ -231,8 +298,23 @@ __global__ void __launch_bounds__(NTHREADS) slab_quant_fp8_kernel(const QuantPar
     lo = __builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], lo, true);
     int hi = __builtin_amdgcn_cvt_pk_fp8_f32(q[4], q[5], 0, false);
     hi = __builtin_amdgcn_cvt_pk_fp8_f32(q[6], q[7], hi, true);
-    *reinterpret_cast<u32x2*>(dst + pp * p.sd[2]) = u32x2{(unsigned)lo, (unsigned)hi};
+    *reinterpret_cast<u32x2*>(dst + q0 * p.sd[2]) = u32x2{(unsigned)lo, (unsigned)hi};
   }
+}
+
+// CUs of the current device (0 if the runtime cannot say), cached per device
+int device_cus() {
+  static int cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (dev >= 0 && dev < 64) {
+    const int c = __atomic_load_n(&cache[dev], __ATOMIC_RELAXED);
+    if (c > 0) return c;
+  }
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  if (dev >= 0 && dev < 64) __atomic_store_n(&cache[dev], cus, __ATOMIC_RELAXED);
+  return cus;
 }
 
 inline bool aligned_to(const void* ptr, uintptr_t a) { return (reinterpret_cast<uintptr_t>(ptr) % a) == 0; }
@@ -260,6 +342,7 @@ int qik_rms_rope(const qik_rms_rope_args* a, void* stream) {
   if (!sizes_ok(a->B, a->S, a->H, a->D)) return QIK_ERR_SHAPE;
   const int64_t rows = a->B * a->S * a->H;
   if (rows == 0) return QIK_OK;
+  if (rows >= (int64_t)INT_MAX) return QIK_ERR_SHAPE;
   if (a->x == nullptr || a->out == nullptr || a->weight == nullptr || a->cos == nullptr || a->sin == nullptr)
     return QIK_ERR_NULL_ARG;
   if (!aligned_to(a->x, 16) || !aligned_to(a->out, 16) || !aligned_to(a->weight, 16) || !aligned_to(a->cos, 16) ||
@@ -274,16 +357,16 @@ int qik_rms_rope(const qik_rms_rope_args* a, void* stream) {
   p.w = a->weight;
   p.cos = a->cos;
   p.sin = a->sin;
-  p.rows = rows;
-  p.S = a->S;
-  p.H = a->H;
+  p.rows = (int)rows;
+  p.S = (int)a->S;
+  p.H = (int)a->H;
   for (int i = 0; i < 3; ++i) {
     p.sx[i] = a->stride_x[i];
     p.so[i] = a->stride_out[i];
   }
   p.eps = a->eps;
   const bool fp16 = a->dtype == QIK_DTYPE_FP16;
-  const int rpb = NTHREADS / (int)(a->D / 8);
+  const int rpb = NTHREADS / (int)(a->D / 8) * RR;
   const int64_t grid = (rows + rpb - 1) / rpb;
   if (grid > (int64_t)UINT_MAX) return QIK_ERR_SHAPE;
   const void* fn;
@@ -331,6 +414,8 @@ int qik_slab_store(const qik_slab_store_args* a, void* stream) {
   cp.P = a->P;
   cp.H = a->H;
   cp.row_bytes = (int)(a->D * 2);
+  cp.zero = fp8 ? a->v_scale : nullptr;
+  cp.nzero = a->B * a->H;
   const int64_t threads = rows * (a->D * 2 / 16);
   const int64_t grid = (threads + NTHREADS - 1) / NTHREADS;
   if (grid > (int64_t)UINT_MAX || a->B * a->H > (int64_t)UINT_MAX) return QIK_ERR_SHAPE;
@@ -349,11 +434,22 @@ int qik_slab_store(const qik_slab_store_args* a, void* stream) {
     qp.sv[i] = a->stride_v[i];
     qp.sd[i] = a->stride_v_dst[i];
   }
-  qp.P = a->P;
-  qp.H = a->H;
-  const void* fn = a->D == 128 ? (const void*)slab_quant_fp8_kernel<128> : (const void*)slab_quant_fp8_kernel<64>;
+  qp.P = (int)a->P;
+  qp.H = (int)a->H;
+  // spread the heads over the device: about two workgroups per CU in total,
+  // at least 32 rows per workgroup, at most 64 workgroups per head
+  const int64_t heads = a->B * a->H;
+  if (heads > (int64_t)(UINT_MAX / 64)) return QIK_ERR_SHAPE;
+  const int cus = device_cus();
+  int64_t chunks = cus > 0 ? 2 * cus / heads : 1;
+  chunks = std::max<int64_t>(1, std::min<int64_t>({chunks, 64, a->P / 32}));
+  qp.chunks = (int)chunks;
   void* qargs[] = {&qp};
-  e = hipLaunchKernel(fn, dim3((unsigned)(a->B * a->H)), dim3(NTHREADS), qargs, 0, s);
+  const void* fs = a->D == 128 ? (const void*)slab_scale_fp8_kernel<128> : (const void*)slab_scale_fp8_kernel<64>;
+  e = hipLaunchKernel(fs, dim3((unsigned)(heads * chunks)), dim3(QTHREADS), qargs, 0, s);
+  if (e != hipSuccess) return QIK_ERR_LAUNCH;
+  const void* fq = a->D == 128 ? (const void*)slab_quant_fp8_kernel<128> : (const void*)slab_quant_fp8_kernel<64>;
+  e = hipLaunchKernel(fq, dim3((unsigned)(heads * chunks)), dim3(QTHREADS), qargs, 0, s);
   return e == hipSuccess ? QIK_OK : QIK_ERR_LAUNCH;
 }
 

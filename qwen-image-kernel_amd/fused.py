@@ -68,19 +68,26 @@ def fused_rms_norm_rope(
     w = weight.to(device=x.device, dtype=torch.float32).contiguous()
     cos, sin = _cos_sin(freqs_cis, x.device)
     out = torch.empty((B, S, H, D), dtype=x.dtype, device=x.device)
+    a = rms_rope_args(x, w, cos, sin, out, eps)
+    with torch.cuda.device(x.device):
+        stream = torch.cuda.current_stream(x.device).cuda_stream
+        _lib.check(_lib.load().qik_rms_rope(ctypes.byref(a), stream), "qik_rms_rope")
+    return out
+
+
+def rms_rope_args(x, weight, cos, sin, out, eps) -> _lib.QikRmsRopeArgs:
+    """The qik_rms_rope argument struct for device tensors (no device work)."""
+    B, S, H, D = x.shape
     a = _lib.QikRmsRopeArgs()
     a.abi_version = _lib.ABI_VERSION
     a.dtype = _DTYPES[x.dtype]
     a.x = x.data_ptr()
     a.out = out.data_ptr()
-    a.weight = w.data_ptr()
+    a.weight = weight.data_ptr()
     a.cos = cos.data_ptr()
     a.sin = sin.data_ptr()
     a.B, a.S, a.H, a.D = B, S, H, D
     a.stride_x = _lib._i64x3(x.stride(0), x.stride(1), x.stride(2))
     a.stride_out = _lib._i64x3(out.stride(0), out.stride(1), out.stride(2))
     a.eps = float(eps)
-    with torch.cuda.device(x.device):
-        stream = torch.cuda.current_stream(x.device).cuda_stream
-        _lib.check(_lib.load().qik_rms_rope(ctypes.byref(a), stream), "qik_rms_rope")
-    return out
+    return a

@@ -56,6 +56,15 @@ class _LayerView:
         c._host_lengths[self._layer] = P
 
     def _store_device(self, k: torch.Tensor, v: torch.Tensor, P: int) -> None:
+        a, keep = self.store_args(k, v, P)
+        kd = self._c.k_buf
+        with torch.cuda.device(kd.device):
+            stream = torch.cuda.current_stream(kd.device).cuda_stream
+            _lib.check(_lib.load().qik_slab_store(ctypes.byref(a), stream), "qik_slab_store")
+        del keep
+
+    def store_args(self, k: torch.Tensor, v: torch.Tensor, P: int):
+        """(qik_slab_store argument struct, tensors it points into) for a device slab."""
         c = self._c
         if k.shape != v.shape or k.dim() != 4 or tuple(k.shape[2:]) != tuple(c.k_buf.shape[2:3] + c.k_buf.shape[4:]):
             raise ValueError(f"k, v must be [B, P, H, D] matching the slab, got {tuple(k.shape)}, {tuple(v.shape)}")
@@ -83,9 +92,7 @@ class _LayerView:
         a.stride_v = _lib._i64x3(v.stride(0), v.stride(1), v.stride(2))
         a.stride_k_dst = _lib._i64x3(kd.stride(0), kd.stride(1), kd.stride(2))
         a.stride_v_dst = _lib._i64x3(vd.stride(0), vd.stride(1), vd.stride(2))
-        with torch.cuda.device(kd.device):
-            stream = torch.cuda.current_stream(kd.device).cuda_stream
-            _lib.check(_lib.load().qik_slab_store(ctypes.byref(a), stream), "qik_slab_store")
+        return a, (k, v)
 
     def _store_torch(self, k: torch.Tensor, v: torch.Tensor, P: int) -> None:
         c = self._c
