@@ -20,6 +20,9 @@ qwen-image-kernel reference repository):
 * ``attention`` -- fp32 explicit-mask attention (triton_attention.py:266-293) extended
                    with fp8 slab V, plus an fp64 brute force for tiny inputs, and the
                    explicit-mask SDPA CPU baseline.
+* ``rms_rope``  -- per-head RMSNorm + RoPE (triton_fused.py:28-105): an fp32 restatement
+                   in the HIP kernel's operation order, and the stock torch composition
+                   the reference tests against (tests/test_fused.py:21-33).
 
 How each function is pinned is stated in its docstring; the tests under
 ``tests/test_oracle_*.py`` hold the checks.
