@@ -370,6 +370,9 @@ def main():
         "roofline": {
             "bound": "mfma",
             "kernel": f"attn_fwd_kernel ({dom})",
+            "launch": ("qik_attn_fwd_ws: one workgroup per resident slot (2 per CU) pulling row "
+                       "blocks from per-XCD queues; the last partial round's row blocks split in two "
+                       "pieces (7/10 and 3/10 of their KV tiles) merged through the workspace"),
             "achieved": round(achieved, 2),
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",

@@ -48,7 +48,8 @@ enum qik_status {
   QIK_ERR_ALIGN = -8,         /* a pointer or stride breaks the 16-byte row-chunk alignment, or K/V rows overlap */
   QIK_ERR_LAUNCH = -9,        /* the HIP launch failed                               */
   QIK_ERR_SEGMENTS = -10,     /* bad segment list for the causal-length builder      */
-  QIK_ERR_DEVICE = -11        /* no usable HIP device / device query failed          */
+  QIK_ERR_DEVICE = -11,       /* no usable HIP device / device query failed          */
+  QIK_ERR_WORKSPACE = -12     /* workspace NULL, misaligned or too small (qik_attn_fwd_ws) */
 };
 
 /* Arguments of one attention call.  Layouts are [B, S, H, D] with the D
@@ -104,6 +105,52 @@ int qik_attn_validate(const qik_attn_args* args);
  * (triton_attention.py:234-259): validates, then enqueues one kernel on
  * `stream`. */
 int qik_attn_fwd(const qik_attn_args* args, void* stream);
+
+/* The first QIK_ATTN_WS_CTL_BYTES bytes of a qik_attn_fwd_ws workspace are its
+ * control words (queue heads, exit and arrival counts) for every shape; the
+ * partial-state slots follow. */
+#define QIK_ATTN_WS_CTL_BYTES 32768
+
+/* Bytes of device workspace qik_attn_fwd_ws needs for `args` on the CURRENT
+ * HIP device (0 only when there is no work).  The workspace holds control
+ * words (queue heads, exit and arrival counts) and the partial softmax states
+ * of split row blocks: the launch runs whole rounds of row blocks, then splits
+ * each row block of the last, partly filled round over its KV tiles into two
+ * pieces (seven tenths and three tenths of its tiles) that the second to finish
+ * combines.  The size depends on the shape and on the device's CU count only,
+ * stays below 2 x (workgroups resident at once) x (BM x D x 4 + 2 KiB)
+ * + 32 KiB (about 70 MB on MI355X, D = 128), and is about 41 MB for
+ * Qwen-Image's 24-head, 4352-row layer.  Host-only (a cached device-attribute
+ * query). */
+int qik_attn_workspace_size(const qik_attn_args* args, int64_t* bytes);
+
+/* qik_attn_fwd for the whole device at once: the launch holds as many
+ * workgroups as the device keeps resident, and they pull row blocks (and the
+ * pieces of split row blocks) from one queue per XCD, so both workgroup
+ * slots of every CU stay busy to the end.  Same arguments and tolerance as
+ * qik_attn_fwd, bit-identical from run to run.  `workspace`: device memory of
+ * the current device, 256-byte aligned, >= qik_attn_workspace_size bytes,
+ * its first QIK_ATTN_WS_CTL_BYTES ZEROED ONCE before its first use (e.g.
+ * hipMemset after allocating it); every launch leaves them zero again, so a
+ * workspace is reused as is, also across shapes and by graph replays.  Launches that may overlap
+ * in time (different streams) need different workspaces.  No workgroup waits
+ * on another.  Replaces the same Triton launch as qik_attn_fwd
+ * (triton_attention.py:234-259); the reference has no workspace. */
+int qik_attn_fwd_ws(const qik_attn_args* args, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Host mirror of the workgroup -> work assignment (no device): for n_items
+ * row blocks (n_row_blocks per (b, h)) and `slots_per_xcd` workgroups
+ * resident per XCD, writes the grid size, the number of split row blocks
+ * (`ngroups`) and, when `pieces` is not NULL, the pieces per split row block;
+ * when item/piece/group are not NULL (cap >= grid entries each), per
+ * workgroup (or, for qik_attn_fwd_ws, queue position loc of XCD x at index
+ * loc * 8 + x): its row block (-1: no work), its piece and its workspace
+ * group (-1: not split).  The second piece of a row block with fewer than 16
+ * KV tiles is skipped on the device (the first runs the whole row block).
+ * `split` = 0 gives qik_attn_fwd's assignment. */
+int qik_attn_work_map(int64_t n_items, int32_t n_row_blocks, int32_t slots_per_xcd, int32_t split,
+                      int32_t* item, int32_t* piece, int32_t* group, int64_t cap, int64_t* grid,
+                      int64_t* ngroups, int32_t* pieces);
 
 /* Host mirror of the KV-tile schedule the kernel runs: for each row block m
  * of BM rows, the number of KV tiles visited, summed over the slab and fresh

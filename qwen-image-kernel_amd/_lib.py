@@ -26,6 +26,9 @@ ABI_VERSION = 1
 DTYPE_BF16 = 0
 DTYPE_FP16 = 1
 
+# leading bytes of a qik_attn_fwd_ws workspace that hold its control words
+WS_CTL_BYTES = 32768
+
 HAS_CACHE = 1
 HAS_KEY_VALID = 2
 UNIFORM_L = 4
@@ -44,6 +47,7 @@ STATUS_NAMES = {
     -9: "QIK_ERR_LAUNCH",
     -10: "QIK_ERR_SEGMENTS",
     -11: "QIK_ERR_DEVICE",
+    -12: "QIK_ERR_WORKSPACE",
 }
 
 _i64x3 = ctypes.c_int64 * 3
@@ -138,6 +142,19 @@ EXPORTS = (
     ("qik_attn_block_shape", ctypes.c_int, (ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32))),
     ("qik_attn_validate", ctypes.c_int, (ctypes.POINTER(QikAttnArgs),)),
     ("qik_attn_fwd", ctypes.c_int, (ctypes.POINTER(QikAttnArgs), ctypes.c_void_p)),
+    ("qik_attn_workspace_size", ctypes.c_int, (ctypes.POINTER(QikAttnArgs), ctypes.POINTER(ctypes.c_int64))),
+    (
+        "qik_attn_fwd_ws",
+        ctypes.c_int,
+        (ctypes.POINTER(QikAttnArgs), ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p),
+    ),
+    (
+        "qik_attn_work_map",
+        ctypes.c_int,
+        (ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p,
+         ctypes.c_void_p, ctypes.c_int64, ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int64),
+         ctypes.POINTER(ctypes.c_int32)),
+    ),
     (
         "qik_attn_tile_schedule",
         ctypes.c_int,

@@ -2,9 +2,9 @@
 
 ``block_causal_flash_attention`` keeps the argument list, defaults, asserts and
 output allocation of ``qwen_image_kernel/triton_attention.py:171-260`` and hands
-the call to the gfx950 HIP kernel through the C ABI (``qik_attn_fwd``).  The
-launch is asynchronous on the current stream of the query's device, like the
-Triton launch it replaces.
+the call to the gfx950 HIP kernel through the C ABI (``qik_attn_fwd_ws``, with
+a workspace kept per device and stream).  The launch is asynchronous on the
+current stream of the query's device, like the Triton launch it replaces.
 
 Also here: ``build_prefix_lengths`` (the per-row causal-length array of
 ``processors.py:22-36``, built on the device in one launch) and
@@ -113,6 +113,7 @@ def block_causal_flash_attention(
     uniform_full: bool = False,  # caller guarantee: L == KV_TOTAL-1 for every row
     *,
     debug_tiles: torch.Tensor | None = None,
+    split_tail: bool = True,
 ) -> torch.Tensor:
     """Exact block-causal attention via per-row prefix lengths.
 
@@ -125,6 +126,12 @@ def block_causal_flash_attention(
 
     ``debug_tiles`` (keyword only, not in the reference) receives the number of
     KV tiles visited per (b, h, row block), int32 [B*H*cdiv(SQ, BM)].
+
+    ``split_tail`` (keyword only, not in the reference): True (default) runs
+    ``qik_attn_fwd_ws`` (resident workgroups pulling row blocks from per-XCD
+    queues, the last partial round's row blocks split in two over their KV
+    tiles) with a zeroed workspace kept per (device, stream); False runs
+    ``qik_attn_fwd``, one workgroup per row block.
     """
     assert query.dtype in (torch.bfloat16, torch.float16), "fp16/bf16 only"
     B, SQ, H, D = query.shape
@@ -179,17 +186,52 @@ def block_causal_flash_attention(
     # with P == 0 the slab (and its fp8 scale) is never read (HAS_CACHE = P > 0, :250)
     args = make_args(query, key, value, L, kv_bytes, out, cache_k if P > 0 else None,
                      cache_v if P > 0 else None, scale if P > 0 else None, uniform, debug_tiles)
-    lib = _lib.load()
     dev = query.device
     if dev.index is not None and dev.index != torch.cuda.current_device():
         with torch.cuda.device(dev):
-            stream = torch.cuda.current_stream(dev).cuda_stream
-            st = lib.qik_attn_fwd(ctypes.byref(args), ctypes.c_void_p(stream))
+            _launch(args, dev, split_tail)
     else:
-        stream = torch.cuda.current_stream(dev).cuda_stream
-        st = lib.qik_attn_fwd(ctypes.byref(args), ctypes.c_void_p(stream))
-    _lib.check(st, "qik_attn_fwd")
+        _launch(args, dev, split_tail)
     return out
+
+
+_WORKSPACES: dict = {}  # (device index, stream handle) -> zeroed uint8 tensor
+
+
+def _workspace(dev: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+    """A workspace for qik_attn_fwd_ws, zeroed when created.
+
+    Every launch leaves the control words zero again, so one workspace per
+    (device, stream) is kept and reused; launches on one stream never overlap.
+    Under graph capture a fresh zeroed workspace is taken from the graph's
+    pool instead (its zeroing is captured too), so a replay never shares the
+    cached one with eager launches.
+    """
+    if torch.cuda.is_current_stream_capturing():
+        return torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+    key = (dev.index, stream)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+        _WORKSPACES[key] = ws
+    return ws
+
+
+def _launch(args: _lib.QikAttnArgs, dev: torch.device, split_tail: bool) -> None:
+    """Enqueue the kernel on the current stream of ``dev`` (the current device)."""
+    lib = _lib.load()
+    handle = torch.cuda.current_stream(dev).cuda_stream
+    stream = ctypes.c_void_p(handle)
+    if not split_tail:
+        _lib.check(lib.qik_attn_fwd(ctypes.byref(args), stream), "qik_attn_fwd")
+        return
+    nbytes = ctypes.c_int64(0)
+    _lib.check(lib.qik_attn_workspace_size(ctypes.byref(args), ctypes.byref(nbytes)), "qik_attn_workspace_size")
+    ws = None if nbytes.value == 0 else _workspace(dev if dev.index is not None else
+                                                   torch.device("cuda", torch.cuda.current_device()),
+                                                   handle, nbytes.value)
+    st = lib.qik_attn_fwd_ws(ctypes.byref(args), None if ws is None else ws.data_ptr(), nbytes.value, stream)
+    _lib.check(st, "qik_attn_fwd_ws")
 
 
 def _norm_slice(start: int, stop: int | None, n: int) -> tuple[int, int]:

@@ -32,9 +32,11 @@
 #include <string.h>
 #include <limits.h>
 #include <algorithm>
+#include <atomic>
 #include <type_traits>
 
 #include "qik_attn.h"
+#include "qik_plan.h"
 
 namespace qik {
 
@@ -42,6 +44,7 @@ typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((__vector_size__(16 * sizeof(float))));
 typedef float f32x2 __attribute__((__vector_size__(2 * sizeof(float))));
+typedef float f32x4 __attribute__((__vector_size__(4 * sizeof(float))));
 typedef __bf16 bf16x8 __attribute__((__vector_size__(8 * sizeof(__bf16))));
 typedef _Float16 f16x8 __attribute__((__vector_size__(8 * sizeof(_Float16))));
 typedef __bf16 bf16x2 __attribute__((__vector_size__(2 * sizeof(__bf16))));
@@ -64,13 +67,30 @@ struct Params {
   const uint8_t* key_valid;
   char* out;
   int32_t* debug_tiles;
+  char* ws_slots;                  // split items: plan.ns partial-state slots per group
+  unsigned* ctl;                   // NULL: one workgroup per unit; else the control words
+                                   // (QIK_ATTN_WS_CTL_BYTES, zero between launches):
+                                   // [0, NXCD) queue heads, [NXCD, 2 NXCD) exits,
+                                   // [2 NXCD, ...) arrivals per group
   int64_t sq[3], skn[3], svn[3], skc[3], svc[3], so[3];  // b, s, h strides in elements
   int64_t svalid_b;
   int SQ, SN, P, H, KV;
-  int n_row_blocks;
   int has_cache, has_key_valid, uniform;
   float qk_scale;
+  WorkPlan plan;
 };
+
+// A split item with fewer than SPLIT_MIN_TILES KV tiles runs whole (its
+// second piece is skipped).  Otherwise piece 0 takes its first
+// (7 T + 5) / 10 tiles and piece 1 the rest.
+constexpr int SPLIT_MIN_TILES = 16;
+
+// Partial softmax state of one thread of a split piece: its DBLK x 16 fp32
+// O^T accumulators (relative to its row's reference point m) and (m, l share).
+template <int D>
+constexpr int slot_oacc_bytes() { return (D / 32) * 16 * 4 * NTHREADS; }
+template <int D>
+constexpr int slot_bytes() { return slot_oacc_bytes<D>() + 8 * NTHREADS; }
 
 __device__ __forceinline__ int cdiv_i(int a, int b) { return (a + b - 1) / b; }
 
@@ -197,8 +217,22 @@ __device__ __forceinline__ void dma_tile(const char* tile, int row_stride, int n
   }
 }
 
+// The kernel arguments, read again from the kernel-argument segment (where
+// the one argument, Params, sits at offset 0).  The empty asm hides that the
+// segment never changes, so every call loads afresh: a value the kernel
+// needs early and late is then not held in an SGPR in between.
+__device__ __forceinline__ Params reread_args() {
+  typedef const __attribute__((address_space(4))) uint32_t* karg_ptr;
+  karg_ptr pk = (karg_ptr)__builtin_amdgcn_kernarg_segment_ptr();
+  asm volatile("" : "+s"(pk));
+  Params p;
+#pragma unroll
+  for (int i = 0; i < (int)(sizeof(Params) / 4); ++i) reinterpret_cast<uint32_t*>(&p)[i] = pk[i];
+  return p;
+}
+
 template <int D, bool FP16, bool V_FP8>
-__global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params p) {
+__global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params args) {
   constexpr int CH = D / 8;              // 16-byte chunks per row (8 elements)
   constexpr int ROWB = D * 2;            // bytes per row of a K/V tile in LDS
   constexpr int KSTEPS = D / 16;         // k-steps of S^T = K.Q^T
@@ -218,6 +252,7 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params p) {
   __shared__ u32x4 sv1[TILE_BYTES / 16];
   __shared__ uint32_t skv[2][BN / 4];           // key_valid bytes of each stage's tile (4 per word)
   __shared__ int sred[NWAVES];
+  __shared__ int snext;                         // queue position handed out to this workgroup
   char* const kst[2] = {reinterpret_cast<char*>(sk0), reinterpret_cast<char*>(sk1)};
   char* const vst[2] = {reinterpret_cast<char*>(sv0), reinterpret_cast<char*>(sv1)};
 
@@ -229,312 +264,422 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params p) {
   const int hf = lane >> 5;   // lane half: keys 4*hf.. of each 8-key group
   const int l32 = lane & 31;
 
-  // ---- work item: XCD-aware remap, then (b,h)-major with row blocks heaviest-first
-  const int G = gridDim.x;
-  const int bid = blockIdx.x;
-  const int xcd = bid & 7, loc = bid >> 3;
-  const int per = G >> 3, rem = G & 7;
-  const int vid = (xcd < rem) ? xcd * (per + 1) + loc : rem * (per + 1) + (xcd - rem) * per + loc;
-  const int nmb = p.n_row_blocks;
-  const int bh = vid / nmb;
-  const int mb = nmb - 1 - (vid - bh * nmb);
-  const int b = bh / p.H;
-  const int h = bh - b * p.H;
-
-  const int m = mb * BM + wave * 32 + l32;  // this lane's query row
-  const bool live = m < p.SQ;
-
-  // ---- causal lengths: this row's L; the block max (dead rows count as -1,
-  // triton_attention.py:82-83); the wave's min and max over live rows.
-  int Lrow = p.KV - 1;
-  if (!p.uniform) Lrow = live ? p.L[m] : -1;
-  int lmax = live ? Lrow : -1;
-  int lmin = live ? Lrow : INT_MAX;
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    lmax = max(lmax, __shfl_xor(lmax, off));
-    lmin = min(lmin, __shfl_xor(lmin, off));
-  }
-  if (lane == 0) sred[wave] = lmax;
-  __syncthreads();
-  int Lmax = sred[0];
-#pragma unroll
-  for (int w = 1; w < NWAVES; ++w) Lmax = max(Lmax, sred[w]);
-  Lmax = __builtin_amdgcn_readfirstlane(Lmax);
-  const int wave_minL = __builtin_amdgcn_readfirstlane(lmin);
-  const int wave_maxL = __builtin_amdgcn_readfirstlane(lmax);
-
-  // ---- KV-tile schedule: tile t of a segment starting at absolute key s0 is
-  // visited iff s0 + t*BN <= Lmax (segment-local tiles, triton_attention.py:97-124).
-  const int s1 = p.has_cache ? p.P : 0;
-  int run0 = 0;
-  if (p.has_cache && Lmax >= 0) run0 = min(cdiv_i(p.P, BN), Lmax / BN + 1);
-  int run1 = 0;
-  if (Lmax >= s1) run1 = min(cdiv_i(p.SN, BN), (Lmax - s1) / BN + 1);
-  const int T = run0 + run1;
-
-  // ---- per-(b,h) segment bases (bytes) and row strides
-  constexpr int VC_ES = V_FP8 ? 1 : 2;
-  const char* const qb = p.q + (b * p.sq[0] + h * p.sq[2]) * 2;
-  const char* const knb = p.k_new + (b * p.skn[0] + h * p.skn[2]) * 2;
-  const char* const vnb = p.v_new + (b * p.svn[0] + h * p.svn[2]) * 2;
-  const char* kcb = nullptr;
-  const char* vcb = nullptr;
-  float vsc = 1.0f;
-  if (p.has_cache) {
-    kcb = p.k_cache + (b * p.skc[0] + h * p.skc[2]) * 2;
-    vcb = p.v_cache + (b * p.svc[0] + h * p.svc[2]) * VC_ES;
-    if constexpr (V_FP8) vsc = p.v_scale[b * p.H + h];
-  }
-  const int kns = (int)(p.skn[1] * 2), vns = (int)(p.svn[1] * 2);
-  const int kcs = (int)(p.skc[1] * 2), vcs = (int)(p.svc[1] * VC_ES);
-  const float qk_scale = p.qk_scale;
-
-  // lane offsets of the tile copies, per segment and tensor
-  const uint32_t koff_new = dma_lane_offset<D>(lane, wave, kns);
-  const uint32_t voff_new = dma_lane_offset<D>(lane, wave, vns);
-  uint32_t koff_c = 0, voff_c = 0;
-  if (p.has_cache) {
-    koff_c = dma_lane_offset<D>(lane, wave, kcs);
-    if constexpr (!V_FP8) voff_c = dma_lane_offset<D>(lane, wave, vcs);
-  }
-
-  // ---- Q as the B operand of S^T = K.Q^T: lane holds Q[m, 16j + 8hf .. +8]
-  u32x4 qreg[KSTEPS];
-  {
-    const char* qr = qb + (int64_t)m * p.sq[1] * 2;
-#pragma unroll
-    for (int j = 0; j < KSTEPS; ++j) {
-      qreg[j] = live ? *reinterpret_cast<const u32x4*>(qr + (16 * j + 8 * hf) * 2)
-                     : u32x4{0u, 0u, 0u, 0u};
+  // ---- units: without a workspace this workgroup's one unit; with one, the
+  // units of this XCD's queue until it runs dry (qik_plan.h).  Nothing waits
+  // on another workgroup: a workgroup that is not resident yet simply starts
+  // later and finds the queue further on.
+  const bool pulled = args.ctl != nullptr;
+  const int xcd = (int)(blockIdx.x % NXCD);
+  for (int first = 1;; first = 0) {
+    int bidv = (int)blockIdx.x;
+    if (pulled) {
+      if (tid == 0) snext = (int)__hip_atomic_fetch_add(args.ctl + xcd, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __syncthreads();
+      const int loc = snext;
+      __syncthreads();  // every thread has read snext before the next unit's head rewrites it
+      if (loc >= args.plan.wpx) break;
+      bidv = loc * NXCD + xcd;
+    } else if (!first) {
+      break;
     }
-  }
+    // the arguments are re-read from the kernel-argument segment for every
+    // unit: kept live across the unit loop instead, they crowd the SGPRs and
+    // the scheduler then serialises the tile loop's LDS reads
+    const Params p = reread_args();
+    const Work wk = plan_work(p.plan, bidv);
+    if (wk.item < 0) continue;
+    const int vid = wk.item;
+    const int nmb = p.plan.nmb;
+    const int bh = vid / nmb;
+    const int mb = nmb - 1 - (vid - bh * nmb);
+    const int b = bh / p.H;
+    const int h = bh - b * p.H;
 
-  // ---- LDS operand offsets inside a stage (lane constants)
-  const int swk = swz<CH>(l32);  // rows l32 and l32 + 32 share it
-  int koffs[KSTEPS];
-#pragma unroll
-  for (int j = 0; j < KSTEPS; ++j) koffs[j] = l32 * ROWB + (((2 * j + hf) ^ swk) << 4);
-  const int j16 = lane & 15;
-  const int rq = 4 * hf + (j16 >> 2);   // V^T read rows: 32*(s>>1) + 16*(s&1) + rq (+8)
-  const int colq = 16 * ((lane >> 4) & 1) + 4 * (j16 & 3);
-  int voffs[2][DBLK];
-#pragma unroll
-  for (int db = 0; db < DBLK; ++db) {
-    const int col = db * 32 + colq;
-    voffs[0][db] = rq * ROWB + (((col >> 3) ^ swz<CH>(rq)) << 4) + ((col & 7) << 1);
-    voffs[1][db] = (rq + 8) * ROWB + (((col >> 3) ^ swz<CH>(rq + 8)) << 4) + ((col & 7) << 1);
-  }
+    const int m = mb * BM + wave * 32 + l32;  // this lane's query row
+    const bool live = m < p.SQ;
 
-  // fp8 slab V goes through registers: two 16-fp8 chunks per thread per tile
-  u32x4 f8reg[F8_LOADS];
-  uint32_t kvbyte = 0;
-
-  auto issue_tile = [&](int g, int stage) {
-    const bool seg0 = g < run0;
-    const int t = seg0 ? g : g - run0;
-    const int row0 = t * BN;
-    const int n_in = (seg0 ? p.P : p.SN) - row0;
-    char* kd = kst[stage];
-    char* vdst = vst[stage];
-    if (seg0) {
-      dma_tile<D>(kcb + (int64_t)row0 * kcs, kcs, n_in, kd, wave, koff_c);
-      if constexpr (V_FP8) {
-        const char* tb = vcb + (int64_t)row0 * vcs;
-        const auto rs = make_rsrc(tb, tile_bytes(n_in, vcs, D));
+    // ---- causal lengths: this row's L; the block max (dead rows count as -1,
+    // triton_attention.py:82-83); the wave's min and max over live rows.
+    int Lrow = p.KV - 1;
+    if (!p.uniform) Lrow = live ? p.L[m] : -1;
+    int lmax = live ? Lrow : -1;
+    int lmin = live ? Lrow : INT_MAX;
 #pragma unroll
-        for (int i = 0; i < F8_LOADS; ++i) {
-          const int qd = i * NTHREADS + tid;
-          const int row = qd / CH8, c16 = qd % CH8;
-          f8reg[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                    rs, (uint32_t)(row * vcs + c16 * 16), 0, 0));
-        }
-      } else {
-        dma_tile<D>(vcb + (int64_t)row0 * vcs, vcs, n_in, vdst, wave, voff_c);
-      }
-    } else {
-      dma_tile<D>(knb + (int64_t)row0 * kns, kns, n_in, kd, wave, koff_new);
-      dma_tile<D>(vnb + (int64_t)row0 * vns, vns, n_in, vdst, wave, voff_new);
+    for (int off = 32; off >= 1; off >>= 1) {
+      lmax = max(lmax, __shfl_xor(lmax, off));
+      lmin = min(lmin, __shfl_xor(lmin, off));
     }
-    if (p.has_key_valid && tid < BN) {
-      // one byte per thread so that bytes past the segment end read as 0 (invalid)
-      const int kv0 = (seg0 ? 0 : s1) + row0;
-      const auto rs = make_rsrc(reinterpret_cast<const char*>(p.key_valid) + b * p.svalid_b + kv0, min(n_in, BN));
-      kvbyte = __builtin_amdgcn_raw_buffer_load_b8(rs, (uint32_t)tid, 0, 0);
-    }
-  };
-  // register-staged parts of a tile: fp8 V dequantised to bf16, key_valid bytes
-  auto finish_tile = [&](int g, int stage) {
-    char* vd = vst[stage];
-    if constexpr (V_FP8) {
-      if (g < run0) {
+    if (lane == 0) sred[wave] = lmax;
+    __syncthreads();
+    int Lmax = sred[0];
 #pragma unroll
-        for (int i = 0; i < F8_LOADS; ++i) {
-          const int qd = i * NTHREADS + tid;
-          const int row = qd / CH8, c16 = qd % CH8;
-          const u32x4 w = f8reg[i];
-          const u32x4 lo = dequant_fp8x8(w.x, w.y, vsc);  // elements 16*c16 .. +7
-          const u32x4 hi = dequant_fp8x8(w.z, w.w, vsc);  // elements 16*c16+8 .. +15
-          *reinterpret_cast<u32x4*>(vd + row * ROWB + (((2 * c16) ^ swz<CH>(row)) << 4)) = lo;
-          *reinterpret_cast<u32x4*>(vd + row * ROWB + (((2 * c16 + 1) ^ swz<CH>(row)) << 4)) = hi;
-        }
-      }
+    for (int w = 1; w < NWAVES; ++w) Lmax = max(Lmax, sred[w]);
+    Lmax = __builtin_amdgcn_readfirstlane(Lmax);
+    const int wave_minL = __builtin_amdgcn_readfirstlane(lmin);
+    const int wave_maxL = __builtin_amdgcn_readfirstlane(lmax);
+
+    // ---- KV-tile schedule: tile t of a segment starting at absolute key s0 is
+    // visited iff s0 + t*BN <= Lmax (segment-local tiles, triton_attention.py:97-124).
+    const int s1 = p.has_cache ? p.P : 0;
+    int run0 = 0;
+    if (p.has_cache && Lmax >= 0) run0 = min(cdiv_i(p.P, BN), Lmax / BN + 1);
+    int run1 = 0;
+    if (Lmax >= s1) run1 = min(cdiv_i(p.SN, BN), (Lmax - s1) / BN + 1);
+    const int T = run0 + run1;
+
+    if (p.debug_tiles != nullptr && tid == 0 && wk.piece == 0) p.debug_tiles[bh * nmb + mb] = T;
+
+    // ---- this unit's tiles [g0, g1): all of them, or one of the item's two
+    // pieces (T, and so the split, is the same for both pieces of the item)
+    const bool split = wk.group >= 0 && T >= SPLIT_MIN_TILES;
+    if (wk.piece > 0 && !split) continue;
+    const int gsplit = (7 * T + 5) / 10;
+    const int g0 = (split && wk.piece) ? gsplit : 0;
+    const int g1 = (split && !wk.piece) ? gsplit : T;
+
+    // ---- per-(b,h) segment bases (bytes) and row strides
+    constexpr int VC_ES = V_FP8 ? 1 : 2;
+    const char* const qb = p.q + (b * p.sq[0] + h * p.sq[2]) * 2;
+    const char* const knb = p.k_new + (b * p.skn[0] + h * p.skn[2]) * 2;
+    const char* const vnb = p.v_new + (b * p.svn[0] + h * p.svn[2]) * 2;
+    const char* kcb = nullptr;
+    const char* vcb = nullptr;
+    float vsc = 1.0f;
+    if (p.has_cache) {
+      kcb = p.k_cache + (b * p.skc[0] + h * p.skc[2]) * 2;
+      vcb = p.v_cache + (b * p.svc[0] + h * p.svc[2]) * VC_ES;
+      if constexpr (V_FP8) vsc = p.v_scale[b * p.H + h];
     }
-    if (p.has_key_valid && tid < BN) reinterpret_cast<uint8_t*>(skv[stage])[tid] = (uint8_t)kvbyte;
-  };
+    const int kns = (int)(p.skn[1] * 2), vns = (int)(p.svn[1] * 2);
+    const int kcs = (int)(p.skc[1] * 2), vcs = (int)(p.svc[1] * VC_ES);
+    const float qk_scale = p.qk_scale;
 
-  float m_run = -INFINITY;  // exp2 reference point of each row (scaled units)
-  float l_run = 0.0f;       // this lane half's share of the running row sum
-  f32x16 oacc[DBLK];
-#pragma unroll
-  for (int db = 0; db < DBLK; ++db) oacc[db] = f32x16{};
+    // lane offsets of the tile copies, per segment and tensor
+    const uint32_t koff_new = dma_lane_offset<D>(lane, wave, kns);
+    const uint32_t voff_new = dma_lane_offset<D>(lane, wave, vns);
+    uint32_t koff_c = 0, voff_c = 0;
+    if (p.has_cache) {
+      koff_c = dma_lane_offset<D>(lane, wave, kcs);
+      if constexpr (!V_FP8) voff_c = dma_lane_offset<D>(lane, wave, vcs);
+    }
 
-  auto compute_tile = [&](int g, int stage) {
-    const char* kS = kst[stage];
-    const char* vS = vst[stage];
-    const bool seg0 = g < run0;
-    const int t = seg0 ? g : g - run0;
-    const int n_in = (seg0 ? p.P : p.SN) - t * BN;  // keys of this tile inside its segment
-    const int kv0 = (seg0 ? 0 : s1) + t * BN;        // absolute index of the tile's first key
-    if (kv0 > wave_maxL) return;                     // no row of this wave sees the tile
-
-    // S^T[n, m] = sum_d K[n, d] Q[m, d]; lane holds m = l32, n = 8(i/4) + 4hf + i%4 (+32)
-    f32x16 sa = f32x16{}, sb = f32x16{};
+    // ---- Q as the B operand of S^T = K.Q^T: lane holds Q[m, 16j + 8hf .. +8]
+    u32x4 qreg[KSTEPS];
     {
-      u32x4 ka0 = lds128(kS + koffs[0]);
-      u32x4 kb0 = lds128(kS + koffs[0] + 32 * ROWB);
+      const char* qr = qb + (int64_t)m * p.sq[1] * 2;
 #pragma unroll
       for (int j = 0; j < KSTEPS; ++j) {
-        u32x4 ka1, kb1;
-        if (j + 1 < KSTEPS) {
-          ka1 = lds128(kS + koffs[j + 1]);
-          kb1 = lds128(kS + koffs[j + 1] + 32 * ROWB);
-        }
-        sa = mfma32<FP16>(ka0, qreg[j], sa);
-        sb = mfma32<FP16>(kb0, qreg[j], sb);
-        if (j + 1 < KSTEPS) {
-          ka0 = ka1;
-          kb0 = kb1;
-        }
+        qreg[j] = live ? *reinterpret_cast<const u32x4*>(qr + (16 * j + 8 * hf) * 2)
+                       : u32x4{0u, 0u, 0u, 0u};
       }
     }
 
-    // mask: segment tail, kv <= L[row], key_valid (triton_attention.py:126-144)
-    const bool full = (n_in >= BN) && (kv0 + BN - 1 <= wave_minL) && !p.has_key_valid;
-    if (!full) {
-      const int lim = min(Lrow - kv0, n_in - 1) - 4 * hf;  // allowed: n_local - 4hf <= lim
-      uint32_t kvw[8];
-      if (p.has_key_valid) {
+    // ---- LDS operand offsets inside a stage (lane constants)
+    const int swk = swz<CH>(l32);  // rows l32 and l32 + 32 share it
+    int koffs[KSTEPS];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) kvw[q] = skv[stage][q * 2 + hf];  // bytes of keys 8q + 4hf .. +3
+    for (int j = 0; j < KSTEPS; ++j) koffs[j] = l32 * ROWB + (((2 * j + hf) ^ swk) << 4);
+    const int j16 = lane & 15;
+    const int rq = 4 * hf + (j16 >> 2);   // V^T read rows: 32*(s>>1) + 16*(s&1) + rq (+8)
+    const int colq = 16 * ((lane >> 4) & 1) + 4 * (j16 & 3);
+    int voffs[2][DBLK];
+#pragma unroll
+    for (int db = 0; db < DBLK; ++db) {
+      const int col = db * 32 + colq;
+      voffs[0][db] = rq * ROWB + (((col >> 3) ^ swz<CH>(rq)) << 4) + ((col & 7) << 1);
+      voffs[1][db] = (rq + 8) * ROWB + (((col >> 3) ^ swz<CH>(rq + 8)) << 4) + ((col & 7) << 1);
+    }
+
+    // fp8 slab V goes through registers: two 16-fp8 chunks per thread per tile
+    u32x4 f8reg[F8_LOADS];
+    uint32_t kvbyte = 0;
+
+    auto issue_tile = [&](int g, int stage) {
+      const bool seg0 = g < run0;
+      const int t = seg0 ? g : g - run0;
+      const int row0 = t * BN;
+      const int n_in = (seg0 ? p.P : p.SN) - row0;
+      char* kd = kst[stage];
+      char* vdst = vst[stage];
+      if (seg0) {
+        dma_tile<D>(kcb + (int64_t)row0 * kcs, kcs, n_in, kd, wave, koff_c);
+        if constexpr (V_FP8) {
+          const char* tb = vcb + (int64_t)row0 * vcs;
+          const auto rs = make_rsrc(tb, tile_bytes(n_in, vcs, D));
+#pragma unroll
+          for (int i = 0; i < F8_LOADS; ++i) {
+            const int qd = i * NTHREADS + tid;
+            const int row = qd / CH8, c16 = qd % CH8;
+            f8reg[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                      rs, (uint32_t)(row * vcs + c16 * 16), 0, 0));
+          }
+        } else {
+          dma_tile<D>(vcb + (int64_t)row0 * vcs, vcs, n_in, vdst, wave, voff_c);
+        }
+      } else {
+        dma_tile<D>(knb + (int64_t)row0 * kns, kns, n_in, kd, wave, koff_new);
+        dma_tile<D>(vnb + (int64_t)row0 * vns, vns, n_in, vdst, wave, voff_new);
       }
+      if (p.has_key_valid && tid < BN) {
+        // one byte per thread so that bytes past the segment end read as 0 (invalid)
+        const int kv0 = (seg0 ? 0 : s1) + row0;
+        const auto rs = make_rsrc(reinterpret_cast<const char*>(p.key_valid) + b * p.svalid_b + kv0, min(n_in, BN));
+        kvbyte = __builtin_amdgcn_raw_buffer_load_b8(rs, (uint32_t)tid, 0, 0);
+      }
+    };
+    // register-staged parts of a tile: fp8 V dequantised to bf16, key_valid bytes
+    auto finish_tile = [&](int g, int stage) {
+      char* vd = vst[stage];
+      if constexpr (V_FP8) {
+        if (g < run0) {
+#pragma unroll
+          for (int i = 0; i < F8_LOADS; ++i) {
+            const int qd = i * NTHREADS + tid;
+            const int row = qd / CH8, c16 = qd % CH8;
+            const u32x4 w = f8reg[i];
+            const u32x4 lo = dequant_fp8x8(w.x, w.y, vsc);  // elements 16*c16 .. +7
+            const u32x4 hi = dequant_fp8x8(w.z, w.w, vsc);  // elements 16*c16+8 .. +15
+            *reinterpret_cast<u32x4*>(vd + row * ROWB + (((2 * c16) ^ swz<CH>(row)) << 4)) = lo;
+            *reinterpret_cast<u32x4*>(vd + row * ROWB + (((2 * c16 + 1) ^ swz<CH>(row)) << 4)) = hi;
+          }
+        }
+      }
+      if (p.has_key_valid && tid < BN) reinterpret_cast<uint8_t*>(skv[stage])[tid] = (uint8_t)kvbyte;
+    };
+
+    float m_run = -INFINITY;  // exp2 reference point of each row (scaled units)
+    float l_run = 0.0f;       // this lane half's share of the running row sum
+    f32x16 oacc[DBLK];
+#pragma unroll
+    for (int db = 0; db < DBLK; ++db) oacc[db] = f32x16{};
+
+    auto compute_tile = [&](int g, int stage) {
+      const char* kS = kst[stage];
+      const char* vS = vst[stage];
+      const bool seg0 = g < run0;
+      const int t = seg0 ? g : g - run0;
+      const int n_in = (seg0 ? p.P : p.SN) - t * BN;  // keys of this tile inside its segment
+      const int kv0 = (seg0 ? 0 : s1) + t * BN;        // absolute index of the tile's first key
+      if (kv0 > wave_maxL) return;                     // no row of this wave sees the tile
+
+      // S^T[n, m] = sum_d K[n, d] Q[m, d]; lane holds m = l32, n = 8(i/4) + 4hf + i%4 (+32)
+      f32x16 sa = f32x16{}, sb = f32x16{};
+      {
+        u32x4 ka0 = lds128(kS + koffs[0]);
+        u32x4 kb0 = lds128(kS + koffs[0] + 32 * ROWB);
+#pragma unroll
+        for (int j = 0; j < KSTEPS; ++j) {
+          u32x4 ka1, kb1;
+          if (j + 1 < KSTEPS) {
+            ka1 = lds128(kS + koffs[j + 1]);
+            kb1 = lds128(kS + koffs[j + 1] + 32 * ROWB);
+          }
+          sa = mfma32<FP16>(ka0, qreg[j], sa);
+          sb = mfma32<FP16>(kb0, qreg[j], sb);
+          if (j + 1 < KSTEPS) {
+            ka0 = ka1;
+            kb0 = kb1;
+          }
+        }
+      }
+
+      // mask: segment tail, kv <= L[row], key_valid (triton_attention.py:126-144)
+      const bool full = (n_in >= BN) && (kv0 + BN - 1 <= wave_minL) && !p.has_key_valid;
+      if (!full) {
+        const int lim = min(Lrow - kv0, n_in - 1) - 4 * hf;  // allowed: n_local - 4hf <= lim
+        uint32_t kvw[8];
+        if (p.has_key_valid) {
+#pragma unroll
+          for (int q = 0; q < 8; ++q) kvw[q] = skv[stage][q * 2 + hf];  // bytes of keys 8q + 4hf .. +3
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int na = 8 * (i >> 2) + (i & 3);
+          bool oka = na <= lim, okb = na + 32 <= lim;
+          if (p.has_key_valid) {
+            oka = oka && ((kvw[i >> 2] >> (8 * (i & 3))) & 0xffu) != 0;
+            okb = okb && ((kvw[4 + (i >> 2)] >> (8 * (i & 3))) & 0xffu) != 0;
+          }
+          sa[i] = oka ? sa[i] : -INFINITY;
+          sb[i] = okb ? sb[i] : -INFINITY;
+        }
+      }
+
+      // online softmax in the exp2 domain (triton_attention.py:146-152); the
+      // reference point moves only when a row max grows by more than TAU, so
+      // p <= 2^TAU and the acc rescale is skipped on most tiles
+      float mx = fmaxf(sa[0], sb[0]);
+#pragma unroll
+      for (int i = 1; i < 16; ++i) mx = fmaxf(fmaxf(mx, sa[i]), sb[i]);
+      mx = pair_max(mx) * qk_scale;
+      if (__any(mx > m_run + TAU)) {
+        const float m_new = fmaxf(m_run, mx);
+        const float alpha = (m_new == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+        l_run *= alpha;
+#pragma unroll
+        for (int db = 0; db < DBLK; ++db)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) oacc[db][i] *= alpha;
+        m_run = m_new;
+      }
+      const float m_safe = (m_run == -INFINITY) ? 0.0f : m_run;
+      float rs = 0.0f;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int na = 8 * (i >> 2) + (i & 3);
-        bool oka = na <= lim, okb = na + 32 <= lim;
-        if (p.has_key_valid) {
-          oka = oka && ((kvw[i >> 2] >> (8 * (i & 3))) & 0xffu) != 0;
-          okb = okb && ((kvw[4 + (i >> 2)] >> (8 * (i & 3))) & 0xffu) != 0;
+        sa[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sa[i], qk_scale, -m_safe));
+        sb[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sb[i], qk_scale, -m_safe));
+        rs += sa[i];
+        rs += sb[i];
+      }
+      l_run += rs;
+
+      // P^T as the B operand: slab s uses registers 8*(s%2).. of block s/2
+      u32x4 pb[SLABS];
+#pragma unroll
+      for (int s = 0; s < SLABS; ++s) {
+        const f32x16& src = (s >> 1) ? sb : sa;
+        const int i0 = (s & 1) * 8;
+        pb[s].x = pack2<FP16>(src[i0 + 0], src[i0 + 1]);
+        pb[s].y = pack2<FP16>(src[i0 + 2], src[i0 + 3]);
+        pb[s].z = pack2<FP16>(src[i0 + 4], src[i0 + 5]);
+        pb[s].w = pack2<FP16>(src[i0 + 6], src[i0 + 7]);
+      }
+
+      // O^T[d, m] += sum_n V[n, d] P[m, n]; the V^T operand comes from the LDS
+      // transpose read: source lane j of each 16-lane group reads row base + j/4,
+      // columns d0 + 4(j%4)..+3, and receives column d0 + j of rows base..base+3
+#pragma unroll
+      for (int s = 0; s < SLABS; ++s) {
+        const int soff = ((s >> 1) * 32 + 16 * (s & 1)) * ROWB;
+#pragma unroll
+        for (int db = 0; db < DBLK; ++db) {
+          const i16x4 x0 = lds_read_tr16(vS + voffs[0][db] + soff);
+          const i16x4 x1 = lds_read_tr16(vS + voffs[1][db] + soff);
+          const u32x2 w0 = __builtin_bit_cast(u32x2, x0);
+          const u32x2 w1 = __builtin_bit_cast(u32x2, x1);
+          oacc[db] = mfma32<FP16>(u32x4{w0.x, w0.y, w1.x, w1.y}, pb[s], oacc[db]);
         }
-        sa[i] = oka ? sa[i] : -INFINITY;
-        sb[i] = okb ? sb[i] : -INFINITY;
+      }
+    };
+
+    if (g0 < g1) {
+      issue_tile(g0, 0);
+      finish_tile(g0, 0);
+    }
+    __syncthreads();
+
+    for (int g = g0; g < g1; g += 2) {
+      // tiles g0, g0 + 2, ... from stage 0, the others from stage 1 (constant LDS offsets)
+      if (g + 1 < g1) issue_tile(g + 1, 1);
+      compute_tile(g, 0);
+      if (g + 1 < g1) finish_tile(g + 1, 1);
+      __syncthreads();
+      if (g + 1 < g1) {
+        if (g + 2 < g1) issue_tile(g + 2, 0);
+        compute_tile(g + 1, 1);
+        if (g + 2 < g1) finish_tile(g + 2, 0);
+        __syncthreads();
       }
     }
 
-    // online softmax in the exp2 domain (triton_attention.py:146-152); the
-    // reference point moves only when a row max grows by more than TAU, so
-    // p <= 2^TAU and the acc rescale is skipped on most tiles
-    float mx = fmaxf(sa[0], sb[0]);
-#pragma unroll
-    for (int i = 1; i < 16; ++i) mx = fmaxf(fmaxf(mx, sa[i]), sb[i]);
-    mx = pair_max(mx) * qk_scale;
-    if (__any(mx > m_run + TAU)) {
-      const float m_new = fmaxf(m_run, mx);
-      const float alpha = (m_new == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
-      l_run *= alpha;
+
+    // ---- split item: both pieces publish their partial state; the second to
+    // arrive combines the two in piece order (so the result does not depend
+    // on which piece that is) and writes the output.  Nothing waits on another
+    // workgroup.  The slots are written with device-scope (sc1, write-through)
+    // stores that complete before the arrival count moves, instead of an
+    // agent-scope fence, which would write back and invalidate the whole L2
+    // that the K/V tiles of the other workgroups live in.  The second piece reads
+    // the other's with plain loads: a slot line is read once per launch, after it was
+    // written, and caches start a launch invalidated, so no cache on the way
+    // can hold an older copy; the pieces of an item come from one XCD's queue,
+    // so the lines are normally still in that XCD's L2.
+    const Params pe = reread_args();
+    float l_part = l_run;
+    if (split) {
+      constexpr int OB = slot_oacc_bytes<D>();
+      constexpr int SB = slot_bytes<D>();
+      constexpr int SC1 = 16;  // cache policy: device scope
+      char* const gslots = pe.ws_slots + (int64_t)wk.group * pe.plan.ns * SB;
+      const auto mine = make_rsrc(gslots + wk.piece * SB, SB);
 #pragma unroll
       for (int db = 0; db < DBLK; ++db)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) oacc[db][i] *= alpha;
-      m_run = m_new;
-    }
-    const float m_safe = (m_run == -INFINITY) ? 0.0f : m_run;
-    float rs = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      sa[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sa[i], qk_scale, -m_safe));
-      sb[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sb[i], qk_scale, -m_safe));
-      rs += sa[i];
-      rs += sb[i];
-    }
-    l_run += rs;
-
-    // P^T as the B operand: slab s uses registers 8*(s%2).. of block s/2
-    u32x4 pb[SLABS];
-#pragma unroll
-    for (int s = 0; s < SLABS; ++s) {
-      const f32x16& src = (s >> 1) ? sb : sa;
-      const int i0 = (s & 1) * 8;
-      pb[s].x = pack2<FP16>(src[i0 + 0], src[i0 + 1]);
-      pb[s].y = pack2<FP16>(src[i0 + 2], src[i0 + 3]);
-      pb[s].z = pack2<FP16>(src[i0 + 4], src[i0 + 5]);
-      pb[s].w = pack2<FP16>(src[i0 + 6], src[i0 + 7]);
-    }
-
-    // O^T[d, m] += sum_n V[n, d] P[m, n]; the V^T operand comes from the LDS
-    // transpose read: source lane j of each 16-lane group reads row base + j/4,
-    // columns d0 + 4(j%4)..+3, and receives column d0 + j of rows base..base+3
-#pragma unroll
-    for (int s = 0; s < SLABS; ++s) {
-      const int soff = ((s >> 1) * 32 + 16 * (s & 1)) * ROWB;
-#pragma unroll
-      for (int db = 0; db < DBLK; ++db) {
-        const i16x4 x0 = lds_read_tr16(vS + voffs[0][db] + soff);
-        const i16x4 x1 = lds_read_tr16(vS + voffs[1][db] + soff);
-        const u32x2 w0 = __builtin_bit_cast(u32x2, x0);
-        const u32x2 w1 = __builtin_bit_cast(u32x2, x1);
-        oacc[db] = mfma32<FP16>(u32x4{w0.x, w0.y, w1.x, w1.y}, pb[s], oacc[db]);
-      }
-    }
-  };
-
-  if (T > 0) {
-    issue_tile(0, 0);
-    finish_tile(0, 0);
-  }
-  __syncthreads();
-
-  for (int g = 0; g < T; g += 2) {
-    // even tile from stage 0, odd tile from stage 1 (constant LDS offsets)
-    if (g + 1 < T) issue_tile(g + 1, 1);
-    compute_tile(g, 0);
-    if (g + 1 < T) finish_tile(g + 1, 1);
-    __syncthreads();
-    if (g + 1 < T) {
-      if (g + 2 < T) issue_tile(g + 2, 0);
-      compute_tile(g + 1, 1);
-      if (g + 2 < T) finish_tile(g + 2, 0);
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const f32x4 v = {oacc[db][4 * q4 + 0], oacc[db][4 * q4 + 1], oacc[db][4 * q4 + 2], oacc[db][4 * q4 + 3]};
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), mine,
+                                                 (uint32_t)(((db * 4 + q4) * NTHREADS + tid) * 16), 0, SC1);
+        }
+      __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f32x2{m_run, l_run}), mine,
+                                            (uint32_t)(OB + tid * 8), 0, SC1);
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the slot has reached device scope
       __syncthreads();
+      if (tid == 0) {
+        // arrival count of the group, 0 between launches: the last piece puts it back
+        unsigned* const word = pe.ctl + 2 * NXCD + wk.group;
+        const unsigned before = __hip_atomic_fetch_add(word, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const bool last = before == 1u;
+        if (last) __hip_atomic_store(word, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        sred[0] = last ? 1 : 0;
+      }
+      __syncthreads();
+      if (sred[0] == 0) continue;  // not the last piece: the last one finishes the item
+
+      // the other piece's state; the two combine in piece order, the same
+      // arithmetic whichever of them arrived last
+      const auto other = make_rsrc(gslots + (wk.piece ^ 1) * SB, SB);
+      const f32x2 mlo = __builtin_bit_cast(
+          f32x2, __builtin_amdgcn_raw_buffer_load_b64(other, (uint32_t)(OB + tid * 8), 0, 0));
+      const bool p1 = wk.piece != 0;
+      const float m0 = p1 ? mlo[0] : m_run, m1 = p1 ? m_run : mlo[0];
+      const float l0 = p1 ? mlo[1] : l_run, l1 = p1 ? l_run : mlo[1];
+      const float mm = fmaxf(m0, m1);
+      const float a0 = (m0 == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m0 - mm);
+      const float a1 = (m1 == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m1 - mm);
+      l_part = l0 * a0 + l1 * a1;
+#pragma unroll
+      for (int db = 0; db < DBLK; ++db)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const f32x4 v = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                        other, (uint32_t)(((db * 4 + q4) * NTHREADS + tid) * 16), 0, 0));
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float o0 = p1 ? v[e] : oacc[db][4 * q4 + e];
+            const float o1 = p1 ? oacc[db][4 * q4 + e] : v[e];
+            oacc[db][4 * q4 + e] = o0 * a0 + o1 * a1;
+          }
+        }
+    }
+
+    // ---- epilogue: out = l > 0 ? acc / l : 0 (triton_attention.py:166-168)
+    const float l_tot = pair_sum(l_part);
+    const float inv = (l_tot > 0.0f) ? 1.0f / l_tot : 0.0f;
+    if (live) {
+      char* orow = pe.out + (b * pe.so[0] + (int64_t)m * pe.so[1] + h * pe.so[2]) * 2;
+#pragma unroll
+      for (int db = 0; db < DBLK; ++db)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const int d = db * 32 + 8 * q4 + 4 * hf;
+          u32x2 w;
+          w.x = pack2<FP16>(oacc[db][4 * q4 + 0] * inv, oacc[db][4 * q4 + 1] * inv);
+          w.y = pack2<FP16>(oacc[db][4 * q4 + 2] * inv, oacc[db][4 * q4 + 3] * inv);
+          *reinterpret_cast<u32x2*>(orow + d * 2) = w;
+        }
+    }
+  }  // units
+
+  // ---- the last workgroup of the XCD to leave puts its queue words back to 0
+  // (every workgroup of the XCD has drawn its last position by then)
+  if (pulled && tid == 0) {
+    const unsigned g = gridDim.x / NXCD;
+    const unsigned before = __hip_atomic_fetch_add(args.ctl + NXCD + xcd, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (before == g - 1) {
+      __hip_atomic_store(args.ctl + xcd, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(args.ctl + NXCD + xcd, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
-
-  // ---- epilogue: out = l > 0 ? acc / l : 0 (triton_attention.py:166-168)
-  const float l_tot = pair_sum(l_run);
-  const float inv = (l_tot > 0.0f) ? 1.0f / l_tot : 0.0f;
-  if (live) {
-    char* orow = p.out + (b * p.so[0] + (int64_t)m * p.so[1] + h * p.so[2]) * 2;
-#pragma unroll
-    for (int db = 0; db < DBLK; ++db)
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const int d = db * 32 + 8 * q4 + 4 * hf;
-        u32x2 w;
-        w.x = pack2<FP16>(oacc[db][4 * q4 + 0] * inv, oacc[db][4 * q4 + 1] * inv);
-        w.y = pack2<FP16>(oacc[db][4 * q4 + 2] * inv, oacc[db][4 * q4 + 3] * inv);
-        *reinterpret_cast<u32x2*>(orow + d * 2) = w;
-      }
-  }
-  if (p.debug_tiles != nullptr && tid == 0) p.debug_tiles[bh * nmb + mb] = T;
 }
 
 // ---------------------------------------------------------------------------
@@ -589,6 +734,135 @@ int schedule_one(int64_t Lmax, int64_t P, int64_t SN, bool has_cache) {
   return (int)(run0 + run1);
 }
 
+// Workgroups one XCD of the current device holds at once for kernel `which`
+// (0..5, see pick_index): occupancy per CU x CUs / NXCD, cached per device.
+constexpr int MAX_DEVICES = 64;
+std::atomic<int> g_slots[MAX_DEVICES][6];
+
+int pick_index(int D, bool fp16, bool vfp8) { return (D == 128 ? 3 : 0) + (fp16 ? 1 : (vfp8 ? 2 : 0)); }
+
+int slots_per_xcd(kernel_fn fn, int which, int* out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return QIK_ERR_DEVICE;
+  if (dev >= 0 && dev < MAX_DEVICES) {
+    const int c = g_slots[dev][which].load(std::memory_order_relaxed);
+    if (c > 0) {
+      *out = c;
+      return QIK_OK;
+    }
+  }
+  int cus = 0, occ = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    return QIK_ERR_DEVICE;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(fn), NTHREADS, 0) !=
+          hipSuccess ||
+      occ <= 0)
+    return QIK_ERR_DEVICE;
+  const int sx = std::max(1, occ * cus / NXCD);
+  if (dev >= 0 && dev < MAX_DEVICES) g_slots[dev][which].store(sx, std::memory_order_relaxed);
+  *out = sx;
+  return QIK_OK;
+}
+
+// Launch geometry of one call.  Without `split`: one workgroup per unit, no
+// workspace.  With it: the last partial round's row blocks split into pieces
+// (qik_plan.h), sx workgroups per XCD pulling units from the XCD's queue, and
+// a workspace of control words (zero between launches) and partial-state
+// slots.
+struct Launch {
+  kernel_fn fn;
+  WorkPlan plan;
+  int64_t grid;
+  int64_t ws_bytes;    // 0: no workspace
+  int64_t ctl_bytes;   // control words at the start of the workspace
+  int slot;
+};
+
+int plan_launch(const qik_attn_args* a, bool split, Launch* L) {
+  const int64_t nmb = cdiv64(a->SQ, BM);
+  const int64_t n = a->B * a->H * nmb;  // <= INT_MAX (qik_attn_validate)
+  const bool fp16 = a->dtype == QIK_DTYPE_FP16;
+  const bool vfp8 = (a->flags & QIK_V_CACHE_FP8) != 0;
+  L->fn = (a->D == 128) ? pick_kernel<128>(fp16, vfp8) : pick_kernel<64>(fp16, vfp8);
+  L->slot = (a->D == 128) ? slot_bytes<128>() : slot_bytes<64>();
+  L->ws_bytes = 0;
+  L->ctl_bytes = 0;
+  L->grid = 0;
+  memset(&L->plan, 0, sizeof(L->plan));
+  if (n == 0) return QIK_OK;
+  int sx = 1;
+  if (split) {
+    const int st = slots_per_xcd(L->fn, pick_index((int)a->D, fp16, vfp8), &sx);
+    if (st != QIK_OK) return st;
+    L->plan = make_plan((int)n, (int)nmb, sx, 1);
+    // queue positions are mapped through loc * NXCD + x, which must fit an
+    // int, and the arrival words must fit the fixed control region (the same
+    // for every shape, so that no launch leaves slot data where another
+    // launch keeps its control words)
+    if ((int64_t)NXCD * L->plan.wpx <= INT_MAX && 2 * NXCD + L->plan.ngroups <= QIK_ATTN_WS_CTL_BYTES / 4) {
+      L->grid = (int64_t)NXCD * std::min(sx, L->plan.wpx);
+      L->ctl_bytes = QIK_ATTN_WS_CTL_BYTES;
+      L->ws_bytes = L->ctl_bytes + (int64_t)L->plan.ngroups * L->plan.ns * L->slot;
+      return QIK_OK;
+    }
+  }
+  L->plan = make_plan((int)n, (int)nmb, sx, 0);
+  L->grid = (int64_t)NXCD * L->plan.wpx;
+  return QIK_OK;
+}
+
+int launch(const qik_attn_args* a, bool split, void* ws, int64_t ws_bytes, void* stream) {
+  const int st = qik_attn_validate(a);
+  if (st != QIK_OK) return st;
+  Launch L;
+  const int pst = plan_launch(a, split, &L);
+  if (pst != QIK_OK) return pst;
+  if (L.grid == 0) return QIK_OK;
+  if (L.ws_bytes > 0 && (ws == nullptr || !aligned_to(ws, 256) || ws_bytes < L.ws_bytes)) return QIK_ERR_WORKSPACE;
+
+  Params p;
+  memset(&p, 0, sizeof(p));
+  p.q = static_cast<const char*>(a->q);
+  p.k_new = static_cast<const char*>(a->k_new);
+  p.v_new = static_cast<const char*>(a->v_new);
+  p.k_cache = static_cast<const char*>(a->k_cache);
+  p.v_cache = static_cast<const char*>(a->v_cache);
+  p.v_scale = a->v_scale;
+  p.L = a->prefix_lengths;
+  p.key_valid = a->key_valid;
+  p.out = static_cast<char*>(a->out);
+  p.debug_tiles = a->debug_tiles;
+  if (L.ws_bytes > 0) {
+    p.ctl = static_cast<unsigned*>(ws);
+    p.ws_slots = static_cast<char*>(ws) + L.ctl_bytes;
+  }
+  for (int i = 0; i < 3; ++i) {
+    p.sq[i] = a->stride_q[i];
+    p.skn[i] = a->stride_k_new[i];
+    p.svn[i] = a->stride_v_new[i];
+    p.skc[i] = a->stride_k_cache[i];
+    p.svc[i] = a->stride_v_cache[i];
+    p.so[i] = a->stride_out[i];
+  }
+  p.svalid_b = a->stride_valid_b;
+  p.SQ = (int)a->SQ;
+  p.SN = (int)a->SN;
+  p.P = (int)a->P;
+  p.H = (int)a->H;
+  p.KV = (int)(a->P + a->SN);
+  p.has_cache = (a->flags & QIK_HAS_CACHE) ? 1 : 0;
+  p.has_key_valid = (a->flags & QIK_HAS_KEY_VALID) ? 1 : 0;
+  p.uniform = (a->flags & QIK_UNIFORM_L) ? 1 : 0;
+  // qk_scale = sm_scale * log2(e), both fp32, as triton_attention.py:93 computes it
+  p.qk_scale = a->sm_scale * 1.44269504088896340736f;
+  p.plan = L.plan;
+
+  void* kargs[] = {&p};
+  const hipError_t e = hipLaunchKernel(reinterpret_cast<const void*>(L.fn), dim3((unsigned)L.grid),
+                                       dim3(NTHREADS), kargs, 0, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? QIK_OK : QIK_ERR_LAUNCH;
+}
+
 }  // namespace qik
 
 extern "C" {
@@ -609,6 +883,7 @@ const char* qik_strerror(int status) {
     case QIK_ERR_LAUNCH: return "HIP kernel launch failed";
     case QIK_ERR_SEGMENTS: return "segments need 0 <= start <= end, and 0 <= prefix_end <= seq_len";
     case QIK_ERR_DEVICE: return "HIP device query failed";
+    case QIK_ERR_WORKSPACE: return "workspace NULL, not 256-byte aligned, or smaller than qik_attn_workspace_size";
     default: return "unknown qik status";
   }
 }
@@ -676,53 +951,43 @@ int qik_attn_validate(const qik_attn_args* a) {
   return QIK_OK;
 }
 
-int qik_attn_fwd(const qik_attn_args* a, void* stream) {
+int qik_attn_fwd(const qik_attn_args* a, void* stream) { return qik::launch(a, false, nullptr, 0, stream); }
+
+int qik_attn_workspace_size(const qik_attn_args* a, int64_t* bytes) {
+  if (bytes == nullptr) return QIK_ERR_NULL_ARG;
+  *bytes = 0;
   const int st = qik_attn_validate(a);
   if (st != QIK_OK) return st;
-  const int64_t nmb = qik::cdiv64(a->SQ, qik::BM);
-  const int64_t grid = a->B * a->H * nmb;
-  if (grid == 0) return QIK_OK;
+  qik::Launch L;
+  const int pst = qik::plan_launch(a, true, &L);
+  if (pst != QIK_OK) return pst;
+  *bytes = L.ws_bytes;
+  return QIK_OK;
+}
 
-  qik::Params p;
-  memset(&p, 0, sizeof(p));
-  p.q = static_cast<const char*>(a->q);
-  p.k_new = static_cast<const char*>(a->k_new);
-  p.v_new = static_cast<const char*>(a->v_new);
-  p.k_cache = static_cast<const char*>(a->k_cache);
-  p.v_cache = static_cast<const char*>(a->v_cache);
-  p.v_scale = a->v_scale;
-  p.L = a->prefix_lengths;
-  p.key_valid = a->key_valid;
-  p.out = static_cast<char*>(a->out);
-  p.debug_tiles = a->debug_tiles;
-  for (int i = 0; i < 3; ++i) {
-    p.sq[i] = a->stride_q[i];
-    p.skn[i] = a->stride_k_new[i];
-    p.svn[i] = a->stride_v_new[i];
-    p.skc[i] = a->stride_k_cache[i];
-    p.svc[i] = a->stride_v_cache[i];
-    p.so[i] = a->stride_out[i];
+int qik_attn_fwd_ws(const qik_attn_args* a, void* workspace, int64_t workspace_bytes, void* stream) {
+  return qik::launch(a, true, workspace, workspace_bytes, stream);
+}
+
+int qik_attn_work_map(int64_t n_items, int32_t n_row_blocks, int32_t slots_per_xcd, int32_t split,
+                      int32_t* item, int32_t* piece, int32_t* group, int64_t cap, int64_t* grid,
+                      int64_t* ngroups, int32_t* pieces) {
+  if (grid == nullptr || ngroups == nullptr) return QIK_ERR_NULL_ARG;
+  if (n_items < 0 || n_items > INT_MAX || n_row_blocks < 1 || slots_per_xcd < 1) return QIK_ERR_SHAPE;
+  const qik::WorkPlan pl = qik::make_plan((int)n_items, n_row_blocks, slots_per_xcd, split ? 1 : 0);
+  *grid = (int64_t)qik::NXCD * pl.wpx;
+  *ngroups = pl.ngroups;
+  if (pieces != nullptr) *pieces = pl.ns;
+  if (item == nullptr && piece == nullptr && group == nullptr) return QIK_OK;
+  if (item == nullptr || piece == nullptr || group == nullptr) return QIK_ERR_NULL_ARG;
+  if (cap < *grid) return QIK_ERR_SHAPE;
+  for (int64_t b = 0; b < *grid; ++b) {
+    const qik::Work w = qik::plan_work(pl, (int)b);
+    item[b] = w.item;
+    piece[b] = w.piece;
+    group[b] = w.group;
   }
-  p.svalid_b = a->stride_valid_b;
-  p.SQ = (int)a->SQ;
-  p.SN = (int)a->SN;
-  p.P = (int)a->P;
-  p.H = (int)a->H;
-  p.KV = (int)(a->P + a->SN);
-  p.n_row_blocks = (int)nmb;
-  p.has_cache = (a->flags & QIK_HAS_CACHE) ? 1 : 0;
-  p.has_key_valid = (a->flags & QIK_HAS_KEY_VALID) ? 1 : 0;
-  p.uniform = (a->flags & QIK_UNIFORM_L) ? 1 : 0;
-  // qk_scale = sm_scale * log2(e), both fp32, as triton_attention.py:93 computes it
-  p.qk_scale = a->sm_scale * 1.44269504088896340736f;
-
-  const bool fp16 = a->dtype == QIK_DTYPE_FP16;
-  const bool vfp8 = (a->flags & QIK_V_CACHE_FP8) != 0;
-  qik::kernel_fn fn = (a->D == 128) ? qik::pick_kernel<128>(fp16, vfp8) : qik::pick_kernel<64>(fp16, vfp8);
-  void* kargs[] = {&p};
-  const hipError_t e = hipLaunchKernel(reinterpret_cast<const void*>(fn), dim3((unsigned)grid),
-                                       dim3(qik::NTHREADS), kargs, 0, static_cast<hipStream_t>(stream));
-  return e == hipSuccess ? QIK_OK : QIK_ERR_LAUNCH;
+  return QIK_OK;
 }
 
 int qik_attn_tile_schedule(int64_t SQ, int64_t P, int64_t SN, int32_t flags, const int32_t* L, int32_t* out) {

@@ -1,0 +1,122 @@
+// Workgroup -> work assignment of the attention kernel, shared by the kernel
+// and the host (launch geometry, workspace size, the work-map export).
+//
+// A work item is one row block (BM query rows of one (b, h)), numbered
+// (b, h)-major with the heaviest row block of a head first.  Workgroups are
+// dealt to the 8 XCDs round-robin (XCD = blockIdx % 8), so XCD x runs the
+// workgroups x, x+8, ...; each XCD gets a contiguous run of items (per + 1 on
+// the first `rem` XCDs, per on the rest) so that a head's K/V stays in one L2.
+//
+// An XCD holds `sx` workgroups at once.  Items that fill whole rounds of sx
+// run as one unit each; each item of the last, partly filled round is split
+// over its KV tiles into two pieces: a big one (the first seven tenths of its
+// tiles) and a small one (the rest).  The order lists the big pieces of all
+// left-over items first, then the small ones.  The launch with a workspace
+// runs sx workgroups per XCD that pull the XCD's units from a queue in this
+// order.  The two workgroups of a CU progress at different rates (the older
+// one's waves win issue arbitration), so the slots of the last whole round
+// free up in two waves: the first takes the big pieces, the second the small
+// ones, and both finish about together (measured on MI355X: 0.6 to 0.75 of
+// the tiles for the big piece are all within 1%), where equal halves leave
+// the early slot idle while the late one finishes.  The two pieces of an item combine
+// their partial softmax states through the workspace slots of its group.
+//
+// plan_work(pl, loc * NXCD + x) is the unit at queue position loc of XCD x;
+// without a workspace the same function maps workgroup bid = loc * NXCD + x.
+
+#pragma once
+
+#include <stdint.h>
+
+#if defined(__HIPCC__)
+#define QIK_HD __host__ __device__
+#else
+#define QIK_HD
+#endif
+
+namespace qik {
+
+constexpr int NXCD = 8;
+constexpr int MAX_PIECES = 2;
+
+struct WorkPlan {
+  int nmb;               // row blocks per (b, h)
+  int per, rem;          // items per XCD: per + 1 on XCDs x < rem, per on the others
+  int full_lo, full_hi;  // items an XCD runs whole when it has per / per + 1 items
+  int ns;                // pieces per split item (1: nothing is split)
+  int wpx;               // workgroups per XCD; grid = NXCD * wpx
+  int mb_major;          // 1: an XCD's items are whole heads, walked rank-major
+  int ngroups;           // split items (workspace slot groups of ns slots)
+};
+
+struct Work {
+  int item;   // row block, or -1 for a workgroup with no work (grid padding)
+  int piece;  // 0 .. ns-1 for a split item, 0 otherwise
+  int group;  // workspace slot group of a split item, -1 otherwise
+};
+
+// Items of an XCD with q items that run whole when it holds sx workgroups.
+QIK_HD inline int plan_full(int q, int sx) { return q >= sx ? sx * (q / sx) : 0; }
+
+// Pieces per split item: two (see above).
+inline int plan_pieces(int r) { return r > 0 ? MAX_PIECES : 1; }
+
+// n items, nmb per (b, h); `split` = 0 runs every item whole.
+inline WorkPlan make_plan(int n, int nmb, int sx, int split) {
+  WorkPlan pl;
+  pl.nmb = nmb;
+  pl.per = n / NXCD;
+  pl.rem = n % NXCD;
+  if (sx < 1) sx = 1;
+  if (split) {
+    pl.full_lo = plan_full(pl.per, sx);
+    pl.full_hi = plan_full(pl.per + 1, sx);
+  } else {
+    pl.full_lo = pl.per;
+    pl.full_hi = pl.per + 1;
+  }
+  const int r_lo = pl.per - pl.full_lo, r_hi = pl.per + 1 - pl.full_hi;
+  const int r_max = (pl.rem > 0 && r_hi > r_lo) ? r_hi : r_lo;
+  pl.ns = plan_pieces(r_max);
+  const int w_lo = pl.full_lo + pl.ns * r_lo;
+  const int w_hi = pl.rem > 0 ? pl.full_hi + pl.ns * r_hi : 0;
+  pl.wpx = w_lo > w_hi ? w_lo : w_hi;
+  pl.ngroups = pl.rem * r_hi + (NXCD - pl.rem) * r_lo;
+  pl.mb_major = (split && pl.rem == 0 && nmb > 0 && pl.per % nmb == 0) ? 1 : 0;
+  return pl;
+}
+
+QIK_HD inline Work plan_work(const WorkPlan& pl, int bid) {
+  const int x = bid % NXCD, loc = bid / NXCD;
+  const int big = x < pl.rem ? 1 : 0;
+  const int q = pl.per + big;
+  const int full = big ? pl.full_hi : pl.full_lo;
+  const int r = q - full;
+  Work w;
+  w.item = -1;
+  w.piece = 0;
+  w.group = -1;
+  if (loc >= full + pl.ns * r) return w;
+  int k = loc;
+  if (loc >= full) {
+    // left-over item t % r, piece t / r: every item's first piece, then every
+    // item's second piece
+    const int t = loc - full;
+    const int nbig = x < pl.rem ? x : pl.rem;
+    k = full + t % r;
+    w.piece = t / r;
+    w.group = nbig * (pl.per + 1 - pl.full_hi) + (x - nbig) * (pl.per - pl.full_lo) + t % r;
+  }
+  const int v0 = x * pl.per + (x < pl.rem ? x : pl.rem);
+  if (pl.mb_major) {
+    // rank-major over the XCD's heads: the heaviest row block of every head
+    // first, the lightest ones (and so the split tail) last
+    const int heads = q / pl.nmb;
+    w.item = v0 + (k % heads) * pl.nmb + k / heads;
+  } else {
+    w.item = v0 + k;
+  }
+  return w;
+}
+
+}  // namespace qik

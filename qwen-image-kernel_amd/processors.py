@@ -7,7 +7,7 @@ kernels:
 
 * Q/K: per-head RMSNorm + RoPE, ``fused_rms_norm_rope`` (qik_rms_rope);
 * prefix extraction: ``layer_cache.store`` (qik_slab_store on a HIP slab);
-* attention: ``block_causal_flash_attention`` (qik_attn_fwd) -- prefill over the
+* attention: ``block_causal_flash_attention`` (qik_attn_fwd_ws) -- prefill over the
   joint sequence with per-row causal lengths from the segment list, decode of
   the target rows against the slab views (no torch.cat), or full attention
   without a cache;

@@ -30,6 +30,12 @@ def header_functions():
     return sorted(names)
 
 
+def test_header_constants_match_the_binding():
+    text = open(HEADER).read()
+    assert re.search(r"#define QIK_ABI_VERSION (\d+)", text).group(1) == str(_lib.ABI_VERSION)
+    assert re.search(r"#define QIK_ATTN_WS_CTL_BYTES (\d+)", text).group(1) == str(_lib.WS_CTL_BYTES)
+
+
 def test_library_loads_and_exports_every_declared_symbol():
     lib = _lib.load()
     names = header_functions()
@@ -121,8 +127,14 @@ def test_validate_error_codes(mutate, code):
     a = _valid_args()
     mutate(a)
     assert _validate(a) == code
-    # qik_attn_fwd validates first and returns the same code without a device call
-    assert _lib.load().qik_attn_fwd(ctypes.byref(a), None) == code
+    # the launches and the workspace query validate first and return the same
+    # code without a device call
+    lib = _lib.load()
+    assert lib.qik_attn_fwd(ctypes.byref(a), None) == code
+    assert lib.qik_attn_fwd_ws(ctypes.byref(a), None, 0, None) == code
+    nbytes = ctypes.c_int64(-1)
+    assert lib.qik_attn_workspace_size(ctypes.byref(a), ctypes.byref(nbytes)) == code
+    assert nbytes.value == 0
     assert _lib.STATUS_NAMES[code] and _lib.strerror(code) != "unknown qik status"
 
 
@@ -135,7 +147,13 @@ def test_fp8_requires_bf16():
 
 def test_fwd_without_work_is_a_no_op():
     a = _valid_args(SQ=0)
-    assert _lib.load().qik_attn_fwd(ctypes.byref(a), None) == 0
+    lib = _lib.load()
+    assert lib.qik_attn_fwd(ctypes.byref(a), None) == 0
+    nbytes = ctypes.c_int64(-1)
+    assert lib.qik_attn_workspace_size(ctypes.byref(a), ctypes.byref(nbytes)) == 0
+    assert nbytes.value == 0
+    assert lib.qik_attn_fwd_ws(ctypes.byref(a), None, 0, None) == 0
+    assert lib.qik_attn_workspace_size(ctypes.byref(a), None) == -1
 
 
 def test_segment_validation_is_host_side():

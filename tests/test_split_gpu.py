@@ -1,0 +1,246 @@
+"""GPU parity of the split last round (qik_attn_fwd_ws).
+
+Each row block of a launch's last, partly filled round runs as two pieces
+over interleaved KV tiles, which meet in a workspace, and the launch's
+resident workgroups pull their units from per-XCD queues.  Checked here
+against the CPU oracle (same bars as the unsplit kernel: max-abs 2e-2,
+mean-abs 2e-3), against the unsplit launch, run to run (bit-identical), with
+rows that see no key in one piece or in any, with garbage in the slots, with
+the control words back at zero after every launch, under HIP-graph replay,
+and the host-side workspace checks.
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oa
+
+import qwen_image_kernel_amd as qik
+import qwen_image_kernel_amd.workloads as wls
+from qwen_image_kernel_amd import _lib
+from qwen_image_kernel_amd.attention import make_args
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS = 2e-2
+MEAN_ABS = 2e-3
+DEV = "cuda"
+
+
+def _flush(msg):
+    print(msg, flush=True)
+
+
+def _rand(shape, gen, scale=1.0):
+    return (torch.randn(*shape, generator=gen) * scale).to(torch.bfloat16)
+
+
+def _check(out, ref, what):
+    o = out.float().cpu().numpy()
+    d = np.abs(o - ref)
+    assert np.isfinite(o).all(), what
+    assert d.max() <= MAX_ABS and d.mean() <= MEAN_ABS, (what, d.max(), d.mean())
+
+
+def _ws_bytes(args):
+    nbytes = ctypes.c_int64()
+    _lib.check(_lib.load().qik_attn_workspace_size(ctypes.byref(args), ctypes.byref(nbytes)), "ws size")
+    return nbytes.value
+
+
+def _plan(n_items, nmb):
+    """(ngroups, pieces) of the split plan on this device: two workgroups per CU."""
+    sx = 2 * torch.cuda.get_device_properties(0).multi_processor_count // 8
+    grid, ngroups, ns = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int32()
+    _lib.check(_lib.load().qik_attn_work_map(n_items, nmb, sx, 1, None, None, None, 0, ctypes.byref(grid),
+                                             ctypes.byref(ngroups), ctypes.byref(ns)), "work map")
+    return ngroups.value, ns.value
+
+
+CTL_BYTES = _lib.WS_CTL_BYTES
+
+
+def _ctl_bytes(ngroups):
+    return CTL_BYTES
+
+
+def _n_groups(args):
+    """Split row blocks of one launch on this device, checked against the workspace size."""
+    nmb = -(-args.SQ // 128)
+    ngroups, ns = _plan(args.B * args.H * nmb, nmb)
+    slot = 128 * args.D * 4 + 256 * 8
+    assert _ws_bytes(args) == _ctl_bytes(ngroups) + ngroups * ns * slot
+    return ngroups
+
+
+def _prefill(name, seed):
+    wl = wls.workload(name)
+    inp = wls.make_inputs(wl, seed=seed, device=DEV, gen_device="cuda")
+    return wl, inp
+
+
+def _run(wl, inp, split):
+    return qik.block_causal_flash_attention(inp["query"], inp["key"], inp["value"], inp["prefix_lengths"], None,
+                                            cache_k=inp["cache_k"], cache_v=inp["cache_v"],
+                                            cache_v_scale=inp["cache_v_scale"], uniform_full=wl.uniform,
+                                            split_tail=split)
+
+
+def test_workspace_size_matches_the_device_plan():
+    """24 heads x 4352 rows: the row blocks left after whole rounds are split."""
+    wl = wls.workload("t2i_1024")
+    q = torch.empty(1, wl.SQ, wl.H, wl.D, dtype=torch.bfloat16, device=DEV)
+    L = torch.zeros(wl.SQ, dtype=torch.int32, device=DEV)
+    a = make_args(q, q, q, L, None, q, None, None, None, False)
+    assert _n_groups(a) > 0
+
+
+@pytest.mark.parametrize("name", ["t2i_512", "multiref_cfg"])
+def test_split_vs_unsplit_vs_oracle(name):
+    _flush(f"case split {name}")
+    wl, inp = _prefill(name, seed=11)
+    a = _run(wl, inp, True)
+    b = _run(wl, inp, False)
+    torch.cuda.synchronize()
+    args = make_args(inp["query"], inp["key"], inp["value"], inp["prefix_lengths"], None, a,
+                     inp["cache_k"], inp["cache_v"], inp["cache_v_scale"], wl.uniform)
+    assert _n_groups(args) > 0
+    d = (a.float() - b.float()).abs()
+    # both within the oracle bar below; between them only the accumulation order differs
+    assert d.max().item() <= 2 * MAX_ABS and d.mean().item() <= 5e-4, (d.max().item(), d.mean().item())
+    heads = list(range(wl.H)) if name == "t2i_512" else [3, 17]
+    slab = {} if wl.P == 0 else dict(cache_k=inp["cache_k"].cpu(), cache_v=inp["cache_v"].cpu(),
+                                     cache_v_scale=inp["cache_v_scale"].cpu())
+    ref = oa.attention_fp32(inp["query"].cpu(), inp["key"].cpu(), inp["value"].cpu(), wl.lengths(), None,
+                            heads=heads, **slab)
+    for h in heads:
+        _check(a[:, :, h], ref[:, :, h], f"{name} h{h} split")
+        _check(b[:, :, h], ref[:, :, h], f"{name} h{h} unsplit")
+
+
+def test_split_is_bit_identical_run_to_run():
+    """Whichever piece arrives last merges, in piece order: the result never changes."""
+    _flush("case split determinism")
+    wl, inp = _prefill("t2i_512", seed=12)
+    outs = [_run(wl, inp, True) for _ in range(4)]
+    for o in outs[1:]:
+        assert torch.equal(outs[0], o)
+
+
+def test_rows_without_keys_in_one_piece_or_any():
+    """1024 keys = 16 tiles, two pieces of 8: rows with L < 512 see nothing in piece 1,
+    rows with L = -1 nothing at all (zeros); key_valid clears piece 0 for batch 1."""
+    _flush("case split empty halves")
+    g = torch.Generator().manual_seed(13)
+    B, SQ, SN, H, D = 2, 640, 1024, 3, 128
+    q, k, v = (_rand((B, n, H, D), g) for n in (SQ, SN, SN))
+    rng = np.random.default_rng(13)
+    L = rng.integers(-1, SN, size=SQ).astype(np.int32)
+    L[:128] = rng.integers(-1, 511, size=128)       # row block 0: never past piece 0
+    L[128:256] = -1                                  # row block 1: empty rows
+    L[256:384:2] = SN - 1                            # row block 2: alternating full / short
+    L[257:384:2] = 40
+    valid = np.ones((B, SN), dtype=bool)
+    valid[1, :512] = False                           # batch 1: piece 0 sees no valid key
+    valid[0, rng.integers(0, SN, 100)] = False
+    kv = torch.from_numpy(valid)
+    Ld = torch.from_numpy(L).to(DEV)
+    a = qik.block_causal_flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), Ld, kv.to(DEV))
+    b = qik.block_causal_flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), Ld, kv.to(DEV), split_tail=False)
+    args = make_args(q.to(DEV), k.to(DEV), v.to(DEV), Ld, kv.to(DEV).to(torch.uint8), a, None, None, None, False)
+    assert _n_groups(args) > 0
+    ref = oa.attention_fp32(q, k, v, L, kv.numpy())
+    _check(a, ref, "split")
+    _check(b, ref, "unsplit")
+    assert (a[:, 128:256].float() == 0).all()
+
+
+def _direct(inp, wl, ws, nbytes):
+    out = torch.empty_like(inp["query"])
+    args = make_args(inp["query"], inp["key"], inp["value"], inp["prefix_lengths"], None, out,
+                     inp["cache_k"], inp["cache_v"], inp["cache_v_scale"], wl.uniform)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    st = _lib.load().qik_attn_fwd_ws(ctypes.byref(args), None if ws is None else ws.data_ptr(), nbytes, stream)
+    return st, out, args
+
+
+@pytest.mark.parametrize("name", ["t2i_512", "edit_768"])
+def test_workspace_control_words_return_to_zero(name):
+    """Only the control words must start at zero: the slots may hold anything.  Every
+    launch leaves the control words zero again, so the next launch reuses the buffer."""
+    _flush(f"case split workspace contents {name}")
+    wl, inp = _prefill(name, seed=14)
+    want = _run(wl, inp, True)
+    _, _, args = _direct(inp, wl, None, 0)
+    n = _ws_bytes(args)
+    nmb = -(-wl.SQ // 128)
+    ctl = _ctl_bytes(_plan(wl.B * wl.H * nmb, nmb)[0])
+    g = torch.Generator(device=DEV).manual_seed(15)
+    ws = torch.randint(0, 256, (n,), generator=g, device=DEV, dtype=torch.int32).to(torch.uint8)
+    ws[:ctl] = 0
+    for i in range(3):
+        st, out, _ = _direct(inp, wl, ws, n)
+        assert st == 0
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), f"launch {i}"
+        assert (ws[:ctl] == 0).all(), f"control words left nonzero after launch {i}"
+
+
+def test_one_workspace_across_shapes():
+    """One workspace, never re-zeroed, through shapes whose split plans differ (a small
+    ragged batch, the 1152-row layer, the multi-reference slab decode): every launch
+    equals a launch on a fresh workspace.  The control words sit in a fixed region,
+    so one shape's slot data never lands where the next keeps its counters."""
+    _flush("case split workspace across shapes")
+    cases = [_prefill("tiny", seed=20), _prefill("t2i_512", seed=21), _prefill("multiref_cfg", seed=22),
+             _prefill("t2i_512", seed=23), _prefill("tiny", seed=24), _prefill("t2i_512", seed=25)]
+    sizes = [_ws_bytes(_direct(inp, wl, None, 0)[2]) for wl, inp in cases]
+    shared = torch.zeros(max(sizes), dtype=torch.uint8, device=DEV)
+    for (wl, inp), n in zip(cases, sizes):
+        fresh = torch.zeros(n, dtype=torch.uint8, device=DEV)
+        st0, want, _ = _direct(inp, wl, fresh, n)
+        st1, got, _ = _direct(inp, wl, shared, n)
+        assert st0 == 0 and st1 == 0
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), wl.name
+        assert (shared[:CTL_BYTES] == 0).all(), wl.name
+
+
+def test_workspace_checks_are_host_side():
+    wl, inp = _prefill("t2i_512", seed=16)
+    _, _, args = _direct(inp, wl, None, 0)
+    n = _ws_bytes(args)
+    ws = torch.zeros(n + 512, dtype=torch.uint8, device=DEV)
+    assert _direct(inp, wl, None, 0)[0] == -12                   # missing
+    assert _direct(inp, wl, ws, n - 1)[0] == -12                 # too small
+    assert _direct(inp, wl, ws[16:], n)[0] == -12                # not 256-byte aligned
+    assert _direct(inp, wl, ws, n)[0] == 0
+    torch.cuda.synchronize()
+
+
+def test_split_under_graph_replay():
+    """Captured once, replayed several times with eager launches (on the cached
+    workspace) between replays: every replay equals the eager result."""
+    _flush("case split graph")
+    wl, inp = _prefill("t2i_512", seed=17)
+    want = _run(wl, inp, True)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        _run(wl, inp, True)  # warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = _run(wl, inp, True)
+    for i in range(4):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), f"replay {i}"
+        eager = _run(wl, inp, True)   # eager launches share nothing with the graph's workspace
+        torch.cuda.synchronize()
+        assert torch.equal(eager, want)

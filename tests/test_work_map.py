@@ -1,0 +1,166 @@
+"""Workgroup -> work assignment of the attention launch (qik_attn_work_map, host only).
+
+The kernel and this export share one function (csrc/qik_plan.h).  Checked here:
+every row block is run exactly once whole or by exactly two pieces (0 and 1)
+that share one workspace group; groups are dense in [0, ngroups); the unsplit
+assignment is the contiguous per-XCD layout; the split one runs whole rounds
+first, then the first (big) piece of every left-over row block, then their
+second pieces; and the workspace size the library reports follows from
+ngroups.
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+
+from qwen_image_kernel_amd import _lib
+
+NXCD = 8
+
+
+def work_map(n, nmb, sx, split):
+    """(item, piece, group, ngroups, ns) per workgroup of the launch."""
+    lib = _lib.load()
+    grid, ngroups, ns = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int32()
+    assert lib.qik_attn_work_map(n, nmb, sx, split, None, None, None, 0, ctypes.byref(grid),
+                                 ctypes.byref(ngroups), ctypes.byref(ns)) == 0
+    g = grid.value
+    item, piece, group = (np.full(max(g, 1), -7, dtype=np.int32) for _ in range(3))
+    st = lib.qik_attn_work_map(n, nmb, sx, split, item.ctypes.data, piece.ctypes.data, group.ctypes.data, g,
+                               ctypes.byref(grid), ctypes.byref(ngroups), None)
+    assert st == 0
+    return item[:g], piece[:g], group[:g], ngroups.value, ns.value
+
+
+def xcd_items(n):
+    per, rem = divmod(n, NXCD)
+    return [per + (1 if x < rem else 0) for x in range(NXCD)]
+
+
+CASES = [
+    # (items, row blocks per head, workgroups per XCD at once)
+    (816, 34, 64),     # 24 heads x 4352 rows on 256 CUs, 2 per CU
+    (768, 32, 64),     # 24 heads x 4096 rows
+    (2784, 58, 64),    # 2 x 24 heads x 7424 rows
+    (216, 9, 64),      # 24 heads x 1152 rows: one partial round
+    (12, 3, 64),       # 4 heads x 320 rows
+    (850, 34, 64),     # 25 heads: uneven XCD runs
+    (377, 29, 64),     # 13 heads x 3712 rows
+    (1, 1, 64),
+    (7, 7, 3),
+    (1024, 32, 64),    # exactly 2 full rounds: nothing to split
+    (1000, 40, 30),    # harvested part: 240 CUs
+]
+
+
+@pytest.mark.parametrize("n,nmb,sx", CASES)
+@pytest.mark.parametrize("split", [0, 1])
+def test_every_row_block_runs_once(n, nmb, sx, split):
+    item, piece, group, ngroups, ns = work_map(n, nmb, sx, split)
+    assert len(item) % NXCD == 0
+    assert ns == (1 if (not split or ngroups == 0) else 2)
+    whole = np.zeros(n, dtype=np.int64)
+    pieces = {}
+    for it, pc, gr in zip(item, piece, group):
+        if it < 0:
+            assert pc == 0 and gr == -1
+            continue
+        assert 0 <= it < n
+        if gr < 0:
+            assert pc == 0
+            whole[it] += 1
+        else:
+            assert 0 <= gr < ngroups and 0 <= pc < ns
+            pieces.setdefault(it, []).append((pc, gr))
+    for it, ps in pieces.items():
+        assert sorted(pc for pc, _ in ps) == list(range(ns)), it
+        assert len({gr for _, gr in ps}) == 1, it
+        assert whole[it] == 0, it
+    covered = whole + np.array([1 if i in pieces else 0 for i in range(n)])
+    assert (covered == 1).all()
+    assert sorted(ps[0][1] for ps in pieces.values()) == list(range(ngroups))
+    if not split:
+        assert ngroups == 0
+
+
+@pytest.mark.parametrize("n,nmb,sx", CASES)
+def test_unsplit_map_is_contiguous_per_xcd(n, nmb, sx):
+    """Workgroup bid runs on XCD bid % 8; XCD x holds a contiguous run of row blocks, in order."""
+    item, _, _, _, _ = work_map(n, nmb, sx, 0)
+    start = 0
+    for x, q in enumerate(xcd_items(n)):
+        mine = item[x::NXCD]
+        assert list(mine[:q]) == list(range(start, start + q))
+        assert (mine[q:] == -1).all()
+        start += q
+
+
+@pytest.mark.parametrize("n,nmb,sx", CASES)
+def test_split_tail_fits_the_slots(n, nmb, sx):
+    """Per XCD: whole rounds of sx row blocks first, then the left-over row blocks' first
+    pieces, then their second pieces in the same order; the XCD keeps the same row
+    blocks as without the split."""
+    item, piece, group, ngroups, ns = work_map(n, nmb, sx, 1)
+    item0, _, _, _, _ = work_map(n, nmb, sx, 0)
+    total = 0
+    for x, q in enumerate(xcd_items(n)):
+        full = sx * (q // sx) if q >= sx else 0
+        r = q - full
+        mine, px, gx = item[x::NXCD], piece[x::NXCD], group[x::NXCD]
+        live = mine[mine >= 0]
+        assert len(live) == full + ns * r
+        assert (gx[:full] == -1).all() and (gx[full:len(live)] >= 0).all()
+        if r:
+            assert list(px[full:len(live)]) == [0] * r + [1] * r
+            assert list(mine[full:full + r]) == list(mine[full + r:full + 2 * r])
+            assert list(gx[full:full + r]) == list(gx[full + r:full + 2 * r])
+        assert set(live.tolist()) == set(item0[x::NXCD][:q].tolist())
+        assert r < sx
+        total += r
+    assert total == ngroups
+
+
+def test_piece_counts_of_the_benchmark_shapes():
+    """256 CUs x 2 workgroups: 24 heads x 4352 rows leave 38 row blocks per XCD after one
+    round of 64, 24 x 4096 rows leave 32; each is split in two."""
+    assert work_map(816, 34, 64, 1)[3:] == (8 * 38, 2)
+    assert work_map(768, 32, 64, 1)[3:] == (8 * 32, 2)
+    assert work_map(1024, 32, 64, 1)[3:] == (0, 1)
+
+
+def test_rank_major_order_puts_light_row_blocks_last():
+    """24 heads x 34 row blocks: each XCD's run is 3 whole heads, walked heaviest row
+    block of every head first, so the split tail holds the lightest ranks."""
+    n, nmb, sx = 816, 34, 64
+    item, piece, _, _, _ = work_map(n, nmb, sx, 1)
+    for x in range(NXCD):
+        mine = item[x::NXCD]
+        live = [i for i, pc in zip(mine, piece[x::NXCD]) if i >= 0 and pc == 0]
+        ranks = [i % nmb for i in live]   # item i % nmb == rank (0 = heaviest row block)
+        assert ranks == sorted(ranks)
+        assert len({i // nmb for i in live}) == 3
+
+
+def test_workspace_size_follows_from_groups():
+    """qik_attn_workspace_size needs a device (CU count): checked on the GPU.  Here the
+    size formula: the fixed 32 KiB of control words (16 queue words + one per group),
+    then ns slots per group of BM x D fp32 accumulators plus (m, l) per thread."""
+    _, _, _, ngroups, ns = work_map(816, 34, 64, 1)
+    slot128 = 128 * 128 * 4 + 256 * 8
+    want = 32768 + ngroups * ns * slot128
+    assert 40e6 < want < 42e6
+    assert 16 + ngroups <= 32768 // 4
+
+
+def test_work_map_rejects_bad_arguments():
+    lib = _lib.load()
+    g, p = ctypes.c_int64(), ctypes.c_int64()
+    assert lib.qik_attn_work_map(10, 0, 64, 1, None, None, None, 0, ctypes.byref(g), ctypes.byref(p), None) == -5
+    assert lib.qik_attn_work_map(10, 5, 0, 1, None, None, None, 0, ctypes.byref(g), ctypes.byref(p), None) == -5
+    assert lib.qik_attn_work_map(-1, 5, 64, 1, None, None, None, 0, ctypes.byref(g), ctypes.byref(p), None) == -5
+    assert lib.qik_attn_work_map(10, 5, 64, 1, None, None, None, 0, None, ctypes.byref(p), None) == -1
+    buf = np.zeros(4, dtype=np.int32)
+    # a buffer shorter than the grid
+    assert lib.qik_attn_work_map(100, 5, 64, 1, buf.ctypes.data, buf.ctypes.data, buf.ctypes.data, 4,
+                                 ctypes.byref(g), ctypes.byref(p), None) == -5
