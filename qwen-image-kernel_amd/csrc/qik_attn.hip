@@ -794,7 +794,7 @@ int plan_launch(const qik_attn_args* a, bool split, Launch* L) {
   if (split) {
     const int st = slots_per_xcd(L->fn, pick_index((int)a->D, fp16, vfp8), &sx);
     if (st != QIK_OK) return st;
-    L->plan = make_plan((int)n, (int)nmb, sx, 1);
+    L->plan = make_plan((int)n, (int)nmb, sx, 1, (a->flags & QIK_UNIFORM_L) ? 0 : 1);
     // queue positions are mapped through loc * NXCD + x, which must fit an
     // int, and the arrival words must fit the fixed control region (the same
     // for every shape, so that no launch leaves slot data where another

@@ -61,8 +61,12 @@ QIK_HD inline int plan_full(int q, int sx) { return q >= sx ? sx * (q / sx) : 0;
 // Pieces per split item: two (see above).
 inline int plan_pieces(int r) { return r > 0 ? MAX_PIECES : 1; }
 
-// n items, nmb per (b, h); `split` = 0 runs every item whole.
-inline WorkPlan make_plan(int n, int nmb, int sx, int split) {
+// n items, nmb per (b, h); `split` = 0 runs every item whole.  `ragged`: the
+// items of a head differ in weight (per-row causal lengths), so an XCD that
+// holds whole heads walks them rank-major (every head's heaviest row block
+// first, the light ones last, where the split tail is); with equal items it
+// keeps them head-major, which holds fewer heads' K/V in its L2 at once.
+inline WorkPlan make_plan(int n, int nmb, int sx, int split, int ragged = 1) {
   WorkPlan pl;
   pl.nmb = nmb;
   pl.per = n / NXCD;
@@ -82,7 +86,7 @@ inline WorkPlan make_plan(int n, int nmb, int sx, int split) {
   const int w_hi = pl.rem > 0 ? pl.full_hi + pl.ns * r_hi : 0;
   pl.wpx = w_lo > w_hi ? w_lo : w_hi;
   pl.ngroups = pl.rem * r_hi + (NXCD - pl.rem) * r_lo;
-  pl.mb_major = (split && pl.rem == 0 && nmb > 0 && pl.per % nmb == 0) ? 1 : 0;
+  pl.mb_major = (split && ragged && pl.rem == 0 && nmb > 0 && pl.per % nmb == 0) ? 1 : 0;
   return pl;
 }
 
