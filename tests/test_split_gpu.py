@@ -121,6 +121,49 @@ def test_split_vs_unsplit_vs_oracle(name):
         _check(b[:, :, h], ref[:, :, h], f"{name} h{h} unsplit")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("D", [64, 128])
+def test_split_dtypes_and_head_dims(dtype, D):
+    """128 text + 1024 image rows over 1152 keys: 18 KV tiles per image row block, so
+    every row block of this one-round launch is split and merged (both pieces
+    non-empty), in both element types and both head dims."""
+    _flush(f"case split dtype={dtype} D={D}")
+    g = torch.Generator().manual_seed(30 + D)
+    segs = [(0, 128, True), (128, 1152, False)]
+    S, H = 1152, 4
+    q, k, v = ((torch.randn(1, S, H, D, generator=g)).to(dtype) for _ in range(3))
+    L = np.arange(S, dtype=np.int32)
+    L[128:] = S - 1
+    Ld = torch.from_numpy(L).to(DEV)
+    out = qik.block_causal_flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), Ld, None)
+    args = make_args(q.to(DEV), k.to(DEV), v.to(DEV), Ld, None, out, None, None, None, False)
+    assert _n_groups(args) > 0
+    assert out.dtype == dtype
+    _check(out, oa.attention_fp32(q, k, v, L), f"{dtype} D={D}")
+    again = qik.block_causal_flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), Ld, None)
+    assert torch.equal(out, again)
+
+
+def test_split_decode_against_fp8_slab():
+    """Decode of 640 target rows against a 512-row fp8 slab + 640 fresh keys (18 tiles,
+    the first 8 from the slab): the split row blocks mix slab and fresh tiles."""
+    _flush("case split fp8 slab decode")
+    g = torch.Generator().manual_seed(40)
+    B, P, SN, H, D = 2, 512, 640, 3, 128
+    pk, pv = ((torch.randn(B, P, H, D, generator=g)).to(torch.bfloat16) for _ in range(2))
+    q, k, v = ((torch.randn(B, SN, H, D, generator=g)).to(torch.bfloat16) for _ in range(3))
+    cache = qik.ContiguousKVCache(1, B, P + 64, H, D, v_fp8=True, device=DEV)
+    cache.get_layer(0).store(pk.to(DEV), pv.to(DEV))
+    kc, vc, sc = cache.get_layer(0).views()
+    L = torch.full((SN,), P + SN - 1, dtype=torch.int32, device=DEV)
+    out = qik.block_causal_flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), L, None, cache_k=kc, cache_v=vc,
+                                           cache_v_scale=sc, uniform_full=True)
+    args = make_args(q.to(DEV), k.to(DEV), v.to(DEV), None, None, out, kc, vc, sc, True)
+    assert _n_groups(args) > 0
+    ref = oa.attention_fp32(q, k, v, L.cpu().numpy(), None, kc.cpu(), vc.cpu(), sc.cpu())
+    _check(out, ref, "fp8 slab decode")
+
+
 def test_split_is_bit_identical_run_to_run():
     """Whichever piece arrives last merges, in piece order: the result never changes."""
     _flush("case split determinism")
