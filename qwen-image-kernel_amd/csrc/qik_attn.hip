@@ -245,12 +245,14 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params args
   constexpr float TAU = 8.0f;            // rescale only when a row max grows by more than 2^8
   static_assert(NBLK == 2, "the S^T code below holds two 32-key blocks");
   static_assert(F8_LOADS >= 1 && F8_LOADS * NTHREADS * 16 == BN * D, "fp8 tile split");
+  static_assert(BN == 64, "one key_valid byte per lane of wave 0");
 
   __shared__ u32x4 sk0[TILE_BYTES / 16];
   __shared__ u32x4 sk1[TILE_BYTES / 16];
   __shared__ u32x4 sv0[TILE_BYTES / 16];
   __shared__ u32x4 sv1[TILE_BYTES / 16];
   __shared__ uint32_t skv[2][BN / 4];           // key_valid bytes of each stage's tile (4 per word)
+  __shared__ int skvall[2];                     // 1 when every key of the stage's tile is valid
   __shared__ int sred[NWAVES];
   __shared__ int snext;                         // queue position handed out to this workgroup
   char* const kst[2] = {reinterpret_cast<char*>(sk0), reinterpret_cast<char*>(sk1)};
@@ -420,11 +422,16 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params args
         dma_tile<D>(knb + (int64_t)row0 * kns, kns, n_in, kd, wave, koff_new);
         dma_tile<D>(vnb + (int64_t)row0 * vns, vns, n_in, vdst, wave, voff_new);
       }
-      if (p.has_key_valid && tid < BN) {
-        // one byte per thread so that bytes past the segment end read as 0 (invalid)
+      if (p.has_key_valid) {
+        // one byte per thread so that bytes past the segment end read as 0
+        // (invalid).  The resource is built before the tid < BN branch and its
+        // size goes through readfirstlane: built inside the branch, the
+        // compiler computes it in VGPRs and loops over the lanes to form it,
+        // with a wait for every load in flight (the tile copies included).
         const int kv0 = (seg0 ? 0 : s1) + row0;
-        const auto rs = make_rsrc(reinterpret_cast<const char*>(p.key_valid) + b * p.svalid_b + kv0, min(n_in, BN));
-        kvbyte = __builtin_amdgcn_raw_buffer_load_b8(rs, (uint32_t)tid, 0, 0);
+        const auto rs = make_rsrc(reinterpret_cast<const char*>(p.key_valid) + b * p.svalid_b + kv0,
+                                  __builtin_amdgcn_readfirstlane(min(n_in, BN)));
+        if (tid < BN) kvbyte = __builtin_amdgcn_raw_buffer_load_b8(rs, (uint32_t)tid, 0, 0);
       }
     };
     // register-staged parts of a tile: fp8 V dequantised to bf16, key_valid bytes
@@ -444,7 +451,12 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params args
           }
         }
       }
-      if (p.has_key_valid && tid < BN) reinterpret_cast<uint8_t*>(skv[stage])[tid] = (uint8_t)kvbyte;
+      if (p.has_key_valid && tid < BN) {
+        // wave 0 holds the tile's BN bytes, one per lane
+        reinterpret_cast<uint8_t*>(skv[stage])[tid] = (uint8_t)kvbyte;
+        const int allv = __all(kvbyte != 0u);
+        if (tid == 0) skvall[stage] = allv;
+      }
     };
 
     float m_run = -INFINITY;  // exp2 reference point of each row (scaled units)
@@ -484,11 +496,14 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params args
       }
 
       // mask: segment tail, kv <= L[row], key_valid (triton_attention.py:126-144)
-      const bool full = (n_in >= BN) && (kv0 + BN - 1 <= wave_minL) && !p.has_key_valid;
+      // a tile whose keys are all valid needs no key_valid term (tail tiles are
+      // never all valid: bytes past the segment end read as 0)
+      const bool kv_mask = p.has_key_valid && __builtin_amdgcn_readfirstlane(skvall[stage]) == 0;
+      const bool full = (n_in >= BN) && (kv0 + BN - 1 <= wave_minL) && !kv_mask;
       if (!full) {
         const int lim = min(Lrow - kv0, n_in - 1) - 4 * hf;  // allowed: n_local - 4hf <= lim
         uint32_t kvw[8];
-        if (p.has_key_valid) {
+        if (kv_mask) {
 #pragma unroll
           for (int q = 0; q < 8; ++q) kvw[q] = skv[stage][q * 2 + hf];  // bytes of keys 8q + 4hf .. +3
         }
@@ -496,7 +511,7 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params args
         for (int i = 0; i < 16; ++i) {
           const int na = 8 * (i >> 2) + (i & 3);
           bool oka = na <= lim, okb = na + 32 <= lim;
-          if (p.has_key_valid) {
+          if (kv_mask) {
             oka = oka && ((kvw[i >> 2] >> (8 * (i & 3))) & 0xffu) != 0;
             okb = okb && ((kvw[4 + (i >> 2)] >> (8 * (i & 3))) & 0xffu) != 0;
           }

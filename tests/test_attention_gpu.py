@@ -199,6 +199,38 @@ def test_all_keys_invalid_gives_zeros():
     _check(out, oa.attention_fp32(q, k, v, L, kv), what="partial key_valid")
 
 
+def test_key_valid_on_some_tiles_only():
+    """A KV tile whose keys are all valid runs without the key_valid term.  A mask
+    that is all true equals no mask bit for bit; padding confined to one tile per
+    batch (fresh keys, then slab and fresh keys of a decode) follows the oracle."""
+    _flush("case key_valid on some tiles")
+    segs, S = ol.make_segments([("text", 256), ("img", 1024)])
+    g = torch.Generator().manual_seed(720)
+    B, H, D = 2, 4, 128
+    q, k, v = (_rand((B, S, H, D), g, 0.3) for _ in range(3))
+    L = ol.build_prefix_lengths(segs, S, S)
+    qd, kd, vd, Ld = q.to(DEV), k.to(DEV), v.to(DEV), torch.from_numpy(L).to(DEV)
+    plain = qik.block_causal_flash_attention(qd, kd, vd, Ld, None)
+    ones = torch.ones(B, S, dtype=torch.bool)
+    assert torch.equal(qik.block_causal_flash_attention(qd, kd, vd, Ld, ones.to(DEV)), plain)
+    kv = ones.clone()
+    kv[0, 200:256] = False      # padded text of batch 0: keys 192-255 are one tile
+    kv[1, 700:710] = False      # a few image keys of batch 1
+    out = qik.block_causal_flash_attention(qd, kd, vd, Ld, kv.to(DEV))
+    _check(out, oa.attention_fp32(q, k, v, L, kv), what="padding in one tile")
+
+    P, T = 320, 256             # decode against a bf16 slab; the mask spans slab + fresh keys
+    ck, cv = (_rand((B, P, H, D), g, 0.3) for _ in range(2))
+    qn, kn, vn = (_rand((B, T, H, D), g, 0.3) for _ in range(3))
+    Lt = np.full(T, P + T - 1, dtype=np.int32)
+    kvd = torch.ones(B, P + T, dtype=torch.bool)
+    kvd[0, 130:140] = False
+    kvd[1, P + 70:P + 75] = False
+    out = qik.block_causal_flash_attention(qn.to(DEV), kn.to(DEV), vn.to(DEV), torch.from_numpy(Lt).to(DEV),
+                                           kvd.to(DEV), cache_k=ck.to(DEV), cache_v=cv.to(DEV))
+    _check(out, oa.attention_fp32(qn, kn, vn, Lt, kvd, ck, cv), what="padding in a slab tile")
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("D", [64, 128])
 def test_dtypes_and_head_dims(dtype, D):
