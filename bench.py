@@ -48,6 +48,9 @@ def parse():
     ap.add_argument("--layers", type=int, default=32, help="layers per shape in one step")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="target duration of the CPU baseline sample (0 disables it)")
+    ap.add_argument("--clock-seconds", type=float, default=1.5,
+                    help="after the timed region, sample the GPU clock for this long under the same "
+                         "launches (0 disables it)")
     ap.add_argument("--only", choices=["t2i_1024", "edit_768"], default=None,
                     help="time one shape only (profiling aid; the default times both)")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
@@ -142,6 +145,117 @@ def cpu_baseline(wls, budget_s: float) -> dict:
                    f"{os.cpu_count()}, {cpu_model()}"),
         "seconds": round(elapsed, 3),
     }
+
+
+def _sysfs_device_dir(dev) -> str | None:
+    """sysfs directory of the HIP device (PCI domain:bus:device.0), or the only card's."""
+    import glob
+
+    import torch
+
+    p = torch.cuda.get_device_properties(dev)
+    cand = f"/sys/bus/pci/devices/{p.pci_domain_id:04x}:{p.pci_bus_id:02x}:{p.pci_device_id:02x}.0"
+    if os.path.exists(os.path.join(cand, "pp_dpm_sclk")):
+        return cand
+    cards = sorted(glob.glob("/sys/class/drm/card*/device/pp_dpm_sclk"))
+    return os.path.dirname(cards[0]) if len(cards) == 1 else None
+
+
+def _read_sclk_mhz(path: str) -> float | None:
+    """The current shader clock from pp_dpm_sclk (the line marked '*', e.g. '1: 2400Mhz *')."""
+    with open(path) as f:
+        for line in f:
+            if line.rstrip().endswith("*"):
+                v = line.split(":", 1)[1].strip().rstrip("*").strip().lower().removesuffix("mhz")
+                return float(v)
+    return None
+
+
+def _read_power_w(ddir: str) -> float | None:
+    import glob
+
+    for name in ("power1_input", "power1_average"):
+        for f in sorted(glob.glob(os.path.join(ddir, "hwmon", "hwmon*", name))):
+            try:
+                with open(f) as fh:
+                    return int(fh.read().strip()) / 1e6
+            except (OSError, ValueError):
+                continue
+    return None
+
+
+def clock_under_load(calls, dev, seconds: float = 1.5) -> dict:
+    """GPU shader clock while the benchmark's own launches keep the GPU busy.
+
+    Runs after the timed region: the step's launches are repeated for about
+    ``seconds`` while a host thread samples the device's sysfs ``pp_dpm_sclk``
+    (and board power) every 20 ms, and ``amd-smi metric --clock`` is run once
+    as a child process for the per-XCD GFX clocks.  Every source is optional.
+    """
+    import re
+    import subprocess
+    import threading
+
+    import torch
+
+    out: dict = {"when": f"{seconds} s of the same launches right after the timed region"}
+    ddir = _sysfs_device_dir(dev)
+    samples, power = [], []
+    stop = threading.Event()
+
+    def sampler():
+        while not stop.is_set():
+            try:
+                v = _read_sclk_mhz(os.path.join(ddir, "pp_dpm_sclk"))
+                if v is not None:
+                    samples.append(v)
+                w = _read_power_w(ddir)
+                if w is not None:
+                    power.append(w)
+            except OSError:
+                return
+            time.sleep(0.02)
+
+    th = threading.Thread(target=sampler, daemon=True) if ddir else None
+    smi: dict = {}
+
+    def run_smi():
+        try:
+            r = subprocess.run(["amd-smi", "metric", "--clock"], capture_output=True, text=True, timeout=20)
+            smi["text"] = r.stdout
+        except (OSError, subprocess.SubprocessError) as e:
+            smi["error"] = type(e).__name__
+
+    sm = threading.Thread(target=run_smi, daemon=True)
+    if th:
+        th.start()
+    t0 = time.perf_counter()
+    started = False
+    while time.perf_counter() - t0 < seconds:
+        for _, fn in calls:
+            fn()
+        if not started and time.perf_counter() - t0 > 0.3:
+            sm.start()
+            started = True
+        torch.cuda.synchronize()
+    stop.set()
+    if th:
+        th.join()
+    if started:
+        sm.join(timeout=25)
+    if samples:
+        s = sorted(samples)
+        out["sysfs_pp_dpm_sclk_mhz"] = {"median": s[len(s) // 2], "min": s[0], "max": s[-1], "samples": len(s),
+                                        "path": os.path.join(ddir, "pp_dpm_sclk")}
+    if power:
+        p = sorted(power)
+        out["board_power_w"] = {"median": round(p[len(p) // 2], 1), "max": round(p[-1], 1)}
+    gfx = [float(x) for x in re.findall(r"GFX_\d+:\s*\n\s*CLK:\s*([\d.]+)\s*MHz", smi.get("text", ""))]
+    if gfx:
+        out["amd_smi_gfx_clk_mhz"] = gfx
+    elif "error" in smi:
+        out["amd_smi"] = smi["error"]
+    return out
 
 
 def _event_us(fn, reps: int) -> float:
@@ -340,6 +454,7 @@ def main():
     dwl = wls.workload(dom)
     achieved = dwl.flops() / (per_workload[dom]["kernel_avg_us"] * 1e-6) / 1e12
 
+    clock = clock_under_load(calls, dev, args.clock_seconds) if args.clock_seconds > 0 else None
     del layers, calls
     sops = side_ops(qik, wls, dev, with_cpu=args.cpu_seconds > 0)
 
@@ -383,6 +498,7 @@ def main():
             "compulsory_bytes_per_launch": dwl.min_bytes(),
         },
         "per_workload": per_workload,
+        "gpu_clock": clock,
         "side_ops": sops,
         "cpu_baseline": cpu,
         "wall_s_timed": round(wall, 3),

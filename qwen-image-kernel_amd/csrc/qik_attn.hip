@@ -231,7 +231,7 @@ __device__ __forceinline__ Params reread_args() {
   return p;
 }
 
-template <int D, bool FP16, bool V_FP8>
+template <int D, bool FP16, bool V_FP8, bool KV>
 __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params args) {
   constexpr int CH = D / 8;              // 16-byte chunks per row (8 elements)
   constexpr int ROWB = D * 2;            // bytes per row of a K/V tile in LDS
@@ -422,7 +422,7 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params args
         dma_tile<D>(knb + (int64_t)row0 * kns, kns, n_in, kd, wave, koff_new);
         dma_tile<D>(vnb + (int64_t)row0 * vns, vns, n_in, vdst, wave, voff_new);
       }
-      if (p.has_key_valid) {
+      if constexpr (KV) {
         // one byte per thread so that bytes past the segment end read as 0
         // (invalid).  The resource is built before the tid < BN branch and its
         // size goes through readfirstlane: built inside the branch, the
@@ -451,7 +451,7 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params args
           }
         }
       }
-      if (p.has_key_valid && tid < BN) {
+      if (KV && tid < BN) {
         // wave 0 holds the tile's BN bytes, one per lane
         reinterpret_cast<uint8_t*>(skv[stage])[tid] = (uint8_t)kvbyte;
         const int allv = __all(kvbyte != 0u);
@@ -498,7 +498,7 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params args
       // mask: segment tail, kv <= L[row], key_valid (triton_attention.py:126-144)
       // a tile whose keys are all valid needs no key_valid term (tail tiles are
       // never all valid: bytes past the segment end read as 0)
-      const bool kv_mask = p.has_key_valid && __builtin_amdgcn_readfirstlane(skvall[stage]) == 0;
+      const bool kv_mask = KV && __builtin_amdgcn_readfirstlane(skvall[stage]) == 0;
       const bool full = (n_in >= BN) && (kv0 + BN - 1 <= wave_minL) && !kv_mask;
       if (!full) {
         const int lim = min(Lrow - kv0, n_in - 1) - 4 * hf;  // allowed: n_local - 4hf <= lim
@@ -722,11 +722,18 @@ __global__ void build_lengths_kernel(const SegList segs, int init, int apply_pre
 
 typedef void (*kernel_fn)(Params);
 
-template <int D>
+template <int D, bool KV>
 kernel_fn pick_kernel(bool fp16, bool vfp8) {
-  if (fp16) return attn_fwd_kernel<D, true, false>;
-  if (vfp8) return attn_fwd_kernel<D, false, true>;
-  return attn_fwd_kernel<D, false, false>;
+  if (fp16) return attn_fwd_kernel<D, true, false, KV>;
+  if (vfp8) return attn_fwd_kernel<D, false, true, KV>;
+  return attn_fwd_kernel<D, false, false, KV>;
+}
+
+// key_valid is a template parameter: without a mask the kernel carries none
+// of its code (the tile loop is then the same as with no mask support at all)
+template <int D>
+kernel_fn pick_kernel(bool fp16, bool vfp8, bool kv) {
+  return kv ? pick_kernel<D, true>(fp16, vfp8) : pick_kernel<D, false>(fp16, vfp8);
 }
 
 inline bool aligned_to(const void* ptr, uintptr_t a) { return (reinterpret_cast<uintptr_t>(ptr) % a) == 0; }
@@ -750,11 +757,13 @@ int schedule_one(int64_t Lmax, int64_t P, int64_t SN, bool has_cache) {
 }
 
 // Workgroups one XCD of the current device holds at once for kernel `which`
-// (0..5, see pick_index): occupancy per CU x CUs / NXCD, cached per device.
+// (0..11, see pick_index): occupancy per CU x CUs / NXCD, cached per device.
 constexpr int MAX_DEVICES = 64;
-std::atomic<int> g_slots[MAX_DEVICES][6];
+std::atomic<int> g_slots[MAX_DEVICES][12];
 
-int pick_index(int D, bool fp16, bool vfp8) { return (D == 128 ? 3 : 0) + (fp16 ? 1 : (vfp8 ? 2 : 0)); }
+int pick_index(int D, bool fp16, bool vfp8, bool kv) {
+  return 2 * ((D == 128 ? 3 : 0) + (fp16 ? 1 : (vfp8 ? 2 : 0))) + (kv ? 1 : 0);
+}
 
 int slots_per_xcd(kernel_fn fn, int which, int* out) {
   int dev = 0;
@@ -798,7 +807,8 @@ int plan_launch(const qik_attn_args* a, bool split, Launch* L) {
   const int64_t n = a->B * a->H * nmb;  // <= INT_MAX (qik_attn_validate)
   const bool fp16 = a->dtype == QIK_DTYPE_FP16;
   const bool vfp8 = (a->flags & QIK_V_CACHE_FP8) != 0;
-  L->fn = (a->D == 128) ? pick_kernel<128>(fp16, vfp8) : pick_kernel<64>(fp16, vfp8);
+  const bool kv = (a->flags & QIK_HAS_KEY_VALID) != 0;
+  L->fn = (a->D == 128) ? pick_kernel<128>(fp16, vfp8, kv) : pick_kernel<64>(fp16, vfp8, kv);
   L->slot = (a->D == 128) ? slot_bytes<128>() : slot_bytes<64>();
   L->ws_bytes = 0;
   L->ctl_bytes = 0;
@@ -807,7 +817,7 @@ int plan_launch(const qik_attn_args* a, bool split, Launch* L) {
   if (n == 0) return QIK_OK;
   int sx = 1;
   if (split) {
-    const int st = slots_per_xcd(L->fn, pick_index((int)a->D, fp16, vfp8), &sx);
+    const int st = slots_per_xcd(L->fn, pick_index((int)a->D, fp16, vfp8, kv), &sx);
     if (st != QIK_OK) return st;
     L->plan = make_plan((int)n, (int)nmb, sx, 1, (a->flags & QIK_UNIFORM_L) ? 0 : 1);
     // queue positions are mapped through loc * NXCD + x, which must fit an
