@@ -199,15 +199,16 @@ def test_all_keys_invalid_gives_zeros():
     _check(out, oa.attention_fp32(q, k, v, L, kv), what="partial key_valid")
 
 
-def test_key_valid_on_some_tiles_only():
+@pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 128), (torch.float16, 64)])
+def test_key_valid_on_some_tiles_only(dtype, D):
     """A KV tile whose keys are all valid runs without the key_valid term.  A mask
     that is all true equals no mask bit for bit; padding confined to one tile per
     batch (fresh keys, then slab and fresh keys of a decode) follows the oracle."""
-    _flush("case key_valid on some tiles")
+    _flush(f"case key_valid on some tiles {dtype} D={D}")
     segs, S = ol.make_segments([("text", 256), ("img", 1024)])
-    g = torch.Generator().manual_seed(720)
-    B, H, D = 2, 4, 128
-    q, k, v = (_rand((B, S, H, D), g, 0.3) for _ in range(3))
+    g = torch.Generator().manual_seed(720 + D)
+    B, H = 2, 4
+    q, k, v = (_rand((B, S, H, D), g, 0.3, dtype) for _ in range(3))
     L = ol.build_prefix_lengths(segs, S, S)
     qd, kd, vd, Ld = q.to(DEV), k.to(DEV), v.to(DEV), torch.from_numpy(L).to(DEV)
     plain = qik.block_causal_flash_attention(qd, kd, vd, Ld, None)
@@ -220,8 +221,8 @@ def test_key_valid_on_some_tiles_only():
     _check(out, oa.attention_fp32(q, k, v, L, kv), what="padding in one tile")
 
     P, T = 320, 256             # decode against a bf16 slab; the mask spans slab + fresh keys
-    ck, cv = (_rand((B, P, H, D), g, 0.3) for _ in range(2))
-    qn, kn, vn = (_rand((B, T, H, D), g, 0.3) for _ in range(3))
+    ck, cv = (_rand((B, P, H, D), g, 0.3, dtype) for _ in range(2))
+    qn, kn, vn = (_rand((B, T, H, D), g, 0.3, dtype) for _ in range(3))
     Lt = np.full(T, P + T - 1, dtype=np.int32)
     kvd = torch.ones(B, P + T, dtype=torch.bool)
     kvd[0, 130:140] = False
@@ -229,6 +230,27 @@ def test_key_valid_on_some_tiles_only():
     out = qik.block_causal_flash_attention(qn.to(DEV), kn.to(DEV), vn.to(DEV), torch.from_numpy(Lt).to(DEV),
                                            kvd.to(DEV), cache_k=ck.to(DEV), cache_v=cv.to(DEV))
     _check(out, oa.attention_fp32(qn, kn, vn, Lt, kvd, ck, cv), what="padding in a slab tile")
+
+
+def test_decode_fp8_slab_head_dim_64_ragged_with_key_valid():
+    """The fp8-slab kernel at D=64 with ragged causal lengths and a key_valid mask
+    over slab and fresh keys; the slab ends inside a tile (200 = 3 x 64 + 8)."""
+    _flush("case fp8 slab D=64 ragged key_valid")
+    B, P, SN, H, D = 2, 200, 130, 3, 64
+    q, kn, vn, ck, cv, cache = _slab_case(B, P, SN, SN, H, D, 730)
+    k8, v8, sc = cache.get_layer(1).views()
+    rng = np.random.default_rng(731)
+    L = np.sort(rng.integers(-1, P + SN, size=SN)).astype(np.int32)
+    kv = torch.ones(B, P + SN, dtype=torch.bool)
+    kv[0, 190:205] = False     # across the slab's end
+    kv[1, P + 60:P + 64] = False
+    kv[1, 5] = False
+    out = qik.block_causal_flash_attention(q.to(DEV), kn.to(DEV), vn.to(DEV), torch.from_numpy(L).to(DEV), kv.to(DEV),
+                                           cache_k=k8, cache_v=v8, cache_v_scale=sc)
+    ref = oa.attention_fp32(q, kn, vn, L, kv, k8.cpu(), v8.cpu(), sc.cpu())
+    _check(out, ref, what="fp8 slab D=64 ragged key_valid")
+    em = oa.flash_emulation(q, kn, vn, L, kv, k8.cpu(), v8.cpu(), sc.cpu())
+    _check(out, em, max_abs=TIGHT_MAX, mean_abs=2e-4, what="vs emulation")
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
