@@ -76,33 +76,42 @@ struct RmsRopeParams {
   float eps;
 };
 
-// One row: x (8 elements of chunk t already in registers) -> 16 output bytes.
+// One row's chunk t: 8 elements of x in fp32, and their sum of squares over the
+// row.  The squares of 16-bit inputs are exact in fp32, so only the additions
+// round: in thread left to right, then a butterfly over the row's TPR lanes
+// (lane t adds lane t^k for k = TPR/2 .. 1).
 template <int D, bool FP16>
-__device__ __forceinline__ u32x4 rms_rope_chunk(const u32x4 raw, const int t, const float (&wv)[8],
-                                                const float4 c4, const float4 s4, const float eps) {
+__device__ __forceinline__ float row_sumsq(const u32x4 raw, float (&x)[8]) {
 #pragma clang fp contract(off)
   constexpr int TPR = D / 8;
-  float x[8];
   unpack2<FP16>(raw.x, x[0], x[1]);
   unpack2<FP16>(raw.y, x[2], x[3]);
   unpack2<FP16>(raw.z, x[4], x[5]);
   unpack2<FP16>(raw.w, x[6], x[7]);
-
-  // sum of squares: the squares of 16-bit inputs are exact in fp32, so only
-  // the additions round; in-thread left to right, then a butterfly over the
-  // row's TPR lanes (lane t adds lane t^k for k = TPR/2 .. 1)
   float ss = x[0] * x[0];
 #pragma unroll
   for (int i = 1; i < 8; ++i) ss = ss + x[i] * x[i];
 #pragma unroll
   for (int k = TPR / 2; k >= 1; k >>= 1) ss = ss + __shfl_xor(ss, k);
+  return ss;
+}
 
-  // r = 1 / sqrt(sum / D + eps): the mean is exact (D a power of two), the
-  // sum with eps rounds in fp32, the square root and the reciprocal are taken
-  // in fp64 (both correctly rounded) and rounded once to fp32
+// r = 1 / sqrt(sum / D + eps): the mean is exact (D a power of two), the sum
+// with eps rounds in fp32, the square root and the reciprocal are taken in fp64
+// (both correctly rounded) and rounded once to fp32.
+template <int D>
+__device__ __forceinline__ float row_rsqrt(const float ss, const float eps) {
+#pragma clang fp contract(off)
   const float ms = ss * (1.0f / (float)D);
-  const float r = (float)(1.0 / sqrt((double)(ms + eps)));
+  return (float)(1.0 / sqrt((double)(ms + eps)));
+}
 
+// The row's chunk t normalised, weighted, rounded to the element type and
+// rotated -> 16 output bytes.
+template <int D, bool FP16>
+__device__ __forceinline__ u32x4 rope_chunk(const float (&x)[8], const float r, const float (&wv)[8],
+                                            const float4 c4, const float4 s4) {
+#pragma clang fp contract(off)
   // n = round((x * r) * w) to the element type, back in fp32 (triton_fused.py:57-58)
   float n[8];
 #pragma unroll
@@ -119,7 +128,6 @@ __device__ __forceinline__ u32x4 rms_rope_chunk(const u32x4 raw, const int t, co
     const float im = e * sn[i] + od * cs[i];
     o[i] = pack2<FP16>(re, im);
   }
-  (void)t;
   return u32x4{o[0], o[1], o[2], o[3]};
 }
 
@@ -143,24 +151,63 @@ __global__ void __launch_bounds__(NTHREADS) rms_rope_kernel(const RmsRopeParams 
   float4 c4[RR], s4[RR];
   int64_t ooff[RR];
   bool live[RR];
+  // (b, s, h) of the first row by division, then stepped by RPB rows with
+  // additions only: the element offsets move by RPB*h-stride, and by the
+  // position (and batch) carries when h (and s) wrap.  64-bit multiplies and
+  // divisions per row made this kernel VALU-bound.
+  int h, s, b;
+  {
+    const int row = min(row0, p.rows - 1);
+    const unsigned bs = (unsigned)row / (unsigned)p.H;
+    h = row - (int)bs * p.H;
+    b = (int)(bs / (unsigned)p.S);
+    s = (int)bs - b * p.S;
+  }
+  int64_t xo = b * p.sx[0] + s * p.sx[1] + h * p.sx[2];
+  int64_t oo = b * p.so[0] + s * p.so[1] + h * p.so[2];
+  const int64_t xh = (int64_t)RPB * p.sx[2], oh = (int64_t)RPB * p.so[2];   // RPB heads on
+  const int64_t xs = p.sx[1] - p.H * p.sx[2], os = p.so[1] - p.H * p.so[2]; // h wraps: next position
+  const int64_t xb = p.sx[0] - p.S * p.sx[1], ob = p.so[0] - p.S * p.so[1]; // s wraps: next batch
 #pragma unroll
   for (int u = 0; u < RR; ++u) {
-    const int row = row0 + u * RPB;
-    live[u] = row < p.rows;
-    const unsigned bs = live[u] ? (unsigned)row / (unsigned)p.H : 0u;
-    const int h = live[u] ? row - (int)bs * p.H : 0;
-    const int b = (int)(bs / (unsigned)p.S);
-    const int s = (int)bs - b * p.S;
+    live[u] = row0 + u * RPB < p.rows;
     raw[u] = u32x4{0u, 0u, 0u, 0u};
-    if (live[u])
-      raw[u] = *reinterpret_cast<const u32x4*>(p.x + (b * p.sx[0] + s * p.sx[1] + h * p.sx[2]) * 2 + t * 16);
+    if (live[u]) raw[u] = *reinterpret_cast<const u32x4*>(p.x + xo * 2 + t * 16);
     c4[u] = *reinterpret_cast<const float4*>(p.cos + s * HALF + 4 * t);
     s4[u] = *reinterpret_cast<const float4*>(p.sin + s * HALF + 4 * t);
-    ooff[u] = (b * p.so[0] + s * p.so[1] + h * p.so[2]) * 2 + t * 16;
+    ooff[u] = oo * 2 + t * 16;
+    if (u + 1 < RR) {
+      h += RPB;
+      xo += xh;
+      oo += oh;
+      while (h >= p.H) {
+        h -= p.H;
+        xo += xs;
+        oo += os;
+        if (++s == p.S) {
+          s = 0;
+          xo += xb;
+          oo += ob;
+        }
+      }
+    }
   }
+  // the RR rows' sums of squares; then one fp64 reciprocal square root per
+  // lane instead of RR: lane t < RR of a row group takes pass t's row, and
+  // every lane fetches its rows' results back from those lanes
+  float x[RR][8], ss[RR];
+#pragma unroll
+  for (int u = 0; u < RR; ++u) ss[u] = row_sumsq<D, FP16>(raw[u], x[u]);
+  static_assert(RR <= TPR, "a row group has a lane per pass");
+  float mine = ss[0];
+#pragma unroll
+  for (int u = 1; u < RR; ++u) mine = (t == u) ? ss[u] : mine;
+  const float rl = row_rsqrt<D>(mine, p.eps);
+  const int g0 = (int)(threadIdx.x % 64) - t;   // first lane of this row group
 #pragma unroll
   for (int u = 0; u < RR; ++u) {
-    const u32x4 o = rms_rope_chunk<D, FP16>(raw[u], t, wv, c4[u], s4[u], p.eps);
+    const float r = __shfl(rl, g0 + u);
+    const u32x4 o = rope_chunk<D, FP16>(x[u], r, wv, c4[u], s4[u]);
     if (live[u]) *reinterpret_cast<u32x4*>(p.out + ooff[u]) = o;
   }
 }
