@@ -348,12 +348,17 @@ def side_ops(qik, wls, dev, with_cpu: bool) -> dict:
     cache = qik.ContiguousKVCache(1, B, P + 272, H, D, v_fp8=True, device=dev)
     layer = cache.get_layer(0)
     sa, keep = layer.store_args(k, v, P)
-    us = _batch_us(lambda: lib.qik_slab_store(ctypes.byref(sa), stream), 50)
+    nws = ctypes.c_int64()
+    _lib.check(lib.qik_slab_store_workspace_size(ctypes.byref(sa), ctypes.byref(nws)), "workspace size")
+    ws = torch.empty(max(nws.value, 4), dtype=torch.uint8, device=dev)
+    us = _batch_us(lambda: lib.qik_slab_store_ws(ctypes.byref(sa), ws.data_ptr(), nws.value, stream), 50)
+    us3 = _batch_us(lambda: lib.qik_slab_store(ctypes.byref(sa), stream), 50)
     api_us = _event_us(lambda: layer.store(k, v), 20)
     nbytes = B * P * H * D * (2 + 2 + 2 + 1) + B * H * 4   # k, v in; k bf16, v fp8 out; scales
     entry = {"shape": [B, P, H, D],
-             "kernels": "slab_copy_kernel + slab_scale_fp8_kernel<128> + slab_quant_fp8_kernel<128>",
+             "kernels": "slab_copy_scale_kernel<128> + slab_quant_fp8_kernel<128> (qik_slab_store_ws)",
              "us": round(us, 2), "api_us": round(api_us, 2), "algorithmic_bytes": nbytes,
+             "us_three_launch_form": round(us3, 2),
              "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
              "frac_hbm": round(nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4)}
     if with_cpu:

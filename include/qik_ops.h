@@ -77,6 +77,18 @@ typedef struct qik_slab_store_args {
 
 int qik_slab_store(const qik_slab_store_args* args, void* stream);
 
+/* The same store in two launches instead of three, for an fp8 V: the K copy and
+ * the scales of the V rows' chunks in one launch, the codes in the second
+ * (replaces the body of _LayerView.store, kv_cache.py:30-45, like
+ * qik_slab_store; the results are bit-identical to it).  The chunks' scales
+ * go to the caller's workspace, at least qik_slab_store_workspace_size bytes,
+ * 4-byte aligned, contents irrelevant (every launch writes what it reads), so
+ * one workspace serves every later call on its stream.  Without an fp8 V it is
+ * qik_slab_store and the workspace may be NULL.  QIK_ERR_WORKSPACE for a
+ * missing, misaligned or short one. */
+int qik_slab_store_workspace_size(const qik_slab_store_args* args, int64_t* bytes);
+int qik_slab_store_ws(const qik_slab_store_args* args, void* workspace, int64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -167,6 +167,9 @@ EXPORTS = (
     ),
     ("qik_rms_rope", ctypes.c_int, (ctypes.POINTER(QikRmsRopeArgs), ctypes.c_void_p)),
     ("qik_slab_store", ctypes.c_int, (ctypes.POINTER(QikSlabStoreArgs), ctypes.c_void_p)),
+    ("qik_slab_store_workspace_size", ctypes.c_int, (ctypes.POINTER(QikSlabStoreArgs), ctypes.POINTER(ctypes.c_int64))),
+    ("qik_slab_store_ws", ctypes.c_int,
+     (ctypes.POINTER(QikSlabStoreArgs), ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p)),
 )
 
 _lock = threading.Lock()

@@ -228,11 +228,9 @@ struct CopyParams {
   int row_bytes;     // D * element size
 };
 
-__global__ void __launch_bounds__(NTHREADS) slab_copy_kernel(const CopyParams p) {
-  const int which = blockIdx.y;
+// One 16-byte chunk g of the copy of tensor `which` (0 = K, 1 = V).
+__device__ __forceinline__ void copy_chunk(const CopyParams& p, const int which, const int64_t g) {
   const int tpr = p.row_bytes / 16;
-  const int64_t g = (int64_t)blockIdx.x * NTHREADS + threadIdx.x;
-  if (p.zero != nullptr && which == 0 && g < p.nzero) p.zero[g] = 0.0f;
   const int64_t row = g / tpr;
   const int t = (int)(g % tpr);
   if (row >= p.rows) return;
@@ -246,6 +244,13 @@ __global__ void __launch_bounds__(NTHREADS) slab_copy_kernel(const CopyParams p)
                             t * 16) = v;
 }
 
+__global__ void __launch_bounds__(NTHREADS) slab_copy_kernel(const CopyParams p) {
+  const int which = blockIdx.y;
+  const int64_t g = (int64_t)blockIdx.x * NTHREADS + threadIdx.x;
+  if (p.zero != nullptr && which == 0 && g < p.nzero) p.zero[g] = 0.0f;
+  copy_chunk(p, which, g);
+}
+
 // fp8 V in two launches over `chunks` workgroups per (b, h), workgroup c
 // owning rows [c*P/chunks, (c+1)*P/chunks) of the head:
 //   slab_scale_fp8_kernel: scale of its rows, max(amax * fp32(1/448), 1e-12),
@@ -257,21 +262,25 @@ struct QuantParams {
   const char* v;     // bf16 [B, P, H, D]
   char* dst;         // fp8 slab V of the layer
   float* scale;      // [B*H]
+  float* partial;    // workspace launches: [B*H*chunks] scales of each chunk's rows (else NULL)
   int64_t sv[3];     // b, p, h (elements)
   int64_t sd[3];     // b, h, p (elements = bytes)
   int P, H, chunks;
 };
 
 constexpr int QTHREADS = 512;
+constexpr int MAX_SCALE_CHUNKS = 64;   // scale chunks per head at most: the workspace holds this many per head
 
+// max(amax * fp32(1/448), 1e-12) of the rows of chunk bx = bh * chunks + c,
+// valid in thread 0 (a block of QTHREADS threads)
 template <int D>
-__global__ void __launch_bounds__(QTHREADS) slab_scale_fp8_kernel(const QuantParams p) {
+__device__ __forceinline__ float chunk_scale(const QuantParams& p, const int bx) {
   constexpr int TPR = D / 8;             // threads per row
   constexpr int RPS = QTHREADS / TPR;    // rows per step
   constexpr int U = 4;                   // steps in flight per thread
   __shared__ float red[QTHREADS / 64];
-  const int bh = blockIdx.x / p.chunks;
-  const int c = blockIdx.x - bh * p.chunks;
+  const int bh = bx / p.chunks;
+  const int c = bx - bh * p.chunks;
   const int h = bh % p.H;
   const int b = bh / p.H;
   const int t = threadIdx.x % TPR;
@@ -303,14 +312,36 @@ __global__ void __launch_bounds__(QTHREADS) slab_scale_fp8_kernel(const QuantPar
   for (int k = 32; k >= 1; k >>= 1) amax = fmaxf(amax, __shfl_xor(amax, k));
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
   __syncthreads();
+  float sc = 0.0f;
   if (threadIdx.x == 0) {
     for (int i = 1; i < QTHREADS / 64; ++i) amax = fmaxf(amax, red[i]);
     amax = fmaxf(amax, red[0]);
-    // torch: amax / 448.0 multiplies by the fp32 reciprocal; clamp_min(1e-12).
-    // Non-negative fp32 values order like their bit patterns.
-    const float sc = fmaxf(amax * (1.0f / 448.0f), 1e-12f);
-    atomicMax(reinterpret_cast<unsigned*>(p.scale) + bh, __float_as_uint(sc));
+    // torch: amax / 448.0 multiplies by the fp32 reciprocal; clamp_min(1e-12)
+    sc = fmaxf(amax * (1.0f / 448.0f), 1e-12f);
   }
+  return sc;
+}
+
+template <int D>
+__global__ void __launch_bounds__(QTHREADS) slab_scale_fp8_kernel(const QuantParams p) {
+  const float sc = chunk_scale<D>(p, blockIdx.x);
+  // non-negative fp32 values order like their bit patterns
+  if (threadIdx.x == 0) atomicMax(reinterpret_cast<unsigned*>(p.scale) + blockIdx.x / p.chunks, __float_as_uint(sc));
+}
+
+// Workspace form, first launch: blocks [0, ncopy) copy K (QTHREADS 16-byte
+// chunks each), the others write their chunk's scale into p.partial.  Every
+// partial is written, so the workspace needs no clearing.
+template <int D>
+__global__ void __launch_bounds__(QTHREADS) slab_copy_scale_kernel(const CopyParams cp, const QuantParams p,
+                                                                   const int ncopy) {
+  if ((int)blockIdx.x < ncopy) {
+    copy_chunk(cp, 0, (int64_t)blockIdx.x * QTHREADS + threadIdx.x);
+    return;
+  }
+  const int bx = (int)blockIdx.x - ncopy;
+  const float sc = chunk_scale<D>(p, bx);
+  if (threadIdx.x == 0) p.partial[bx] = sc;
 }
 
 template <int D>
@@ -328,7 +359,16 @@ __global__ void __launch_bounds__(QTHREADS) slab_quant_fp8_kernel(const QuantPar
   const int64_t rs = p.sv[1] * 2;
   const int p0 = (int)((int64_t)p.P * c / p.chunks);
   const int p1 = (int)((int64_t)p.P * (c + 1) / p.chunks);
-  const float scale = p.scale[bh];
+  float scale;
+  if (p.partial != nullptr) {
+    // the head's scale is the largest of its chunks' (amax -> scale is
+    // monotone, rounding included); chunk 0 also stores it
+    scale = 0.0f;
+    for (int i = 0; i < p.chunks; ++i) scale = fmaxf(scale, p.partial[bh * p.chunks + i]);
+    if (c == 0 && threadIdx.x == 0) p.scale[bh] = scale;
+  } else {
+    scale = p.scale[bh];
+  }
   char* dst = p.dst + b * p.sd[0] + h * p.sd[1] + t * 8;
   for (int q0 = p0 + r0; q0 < p1; q0 += RPS) {
     const u32x4 raw = *reinterpret_cast<const u32x4*>(src + q0 * rs);
@@ -425,8 +465,12 @@ int qik_rms_rope(const qik_rms_rope_args* a, void* stream) {
   return e == hipSuccess ? QIK_OK : QIK_ERR_LAUNCH;
 }
 
-int qik_slab_store(const qik_slab_store_args* a, void* stream) {
-  using namespace qik_ops;
+}  // extern "C"
+
+namespace qik_ops {
+
+// Checks of qik_slab_store's arguments; rows = B*H*P on success.
+int validate_store(const qik_slab_store_args* a, int64_t* rows) {
   if (a == nullptr) return QIK_ERR_NULL_ARG;
   if (a->abi_version != QIK_ABI_VERSION || a->reserved0 != 0) return QIK_ERR_ABI_VERSION;
   if (a->dtype != QIK_DTYPE_BF16 && a->dtype != QIK_DTYPE_FP16) return QIK_ERR_DTYPE;
@@ -435,15 +479,25 @@ int qik_slab_store(const qik_slab_store_args* a, void* stream) {
   if (fp8 != (a->v_scale != nullptr)) return QIK_ERR_FP8_SCALE;
   if (a->D != 64 && a->D != 128) return QIK_ERR_HEAD_DIM;
   if (!sizes_ok(a->B, a->P, a->H, a->D)) return QIK_ERR_SHAPE;
-  const int64_t rows = a->B * a->H * a->P;
-  if (rows == 0) return QIK_OK;
+  *rows = a->B * a->H * a->P;
+  if (*rows == 0) return QIK_OK;
   if (a->k == nullptr || a->v == nullptr || a->k_dst == nullptr || a->v_dst == nullptr) return QIK_ERR_NULL_ARG;
   if (!aligned_to(a->k, 16) || !aligned_to(a->v, 16) || !aligned_to(a->k_dst, 16)) return QIK_ERR_ALIGN;
   if (!aligned_to(a->v_dst, fp8 ? 8 : 16)) return QIK_ERR_ALIGN;
   if (!strides_ok(a->stride_k, 8) || !strides_ok(a->stride_v, 8) || !strides_ok(a->stride_k_dst, 8) ||
       !strides_ok(a->stride_v_dst, 8))
     return QIK_ERR_ALIGN;
-  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (a->B * a->H > (int64_t)(UINT_MAX / MAX_SCALE_CHUNKS)) return QIK_ERR_SHAPE;
+  return QIK_OK;
+}
+
+// The store; `partial` (B*H*MAX_SCALE_CHUNKS floats or more) selects the
+// two-launch form for an fp8 V, NULL the three-launch one.
+int store(const qik_slab_store_args* a, float* partial, hipStream_t s) {
+  int64_t rows = 0;
+  const int st = validate_store(a, &rows);
+  if (st != QIK_OK || rows == 0) return st;
+  const bool fp8 = a->v_fp8 != 0;
 
   CopyParams cp;
   memset(&cp, 0, sizeof(cp));
@@ -461,22 +515,18 @@ int qik_slab_store(const qik_slab_store_args* a, void* stream) {
   cp.P = a->P;
   cp.H = a->H;
   cp.row_bytes = (int)(a->D * 2);
-  cp.zero = fp8 ? a->v_scale : nullptr;
+  cp.zero = (fp8 && partial == nullptr) ? a->v_scale : nullptr;
   cp.nzero = a->B * a->H;
   const int64_t threads = rows * (a->D * 2 / 16);
   const int64_t grid = (threads + NTHREADS - 1) / NTHREADS;
-  if (grid > (int64_t)UINT_MAX || a->B * a->H > (int64_t)UINT_MAX) return QIK_ERR_SHAPE;
-  void* cargs[] = {&cp};
-  hipError_t e = hipLaunchKernel(reinterpret_cast<const void*>(slab_copy_kernel), dim3((unsigned)grid, fp8 ? 1 : 2),
-                                 dim3(NTHREADS), cargs, 0, s);
-  if (e != hipSuccess) return QIK_ERR_LAUNCH;
-  if (!fp8) return QIK_OK;
+  if (grid > (int64_t)UINT_MAX) return QIK_ERR_SHAPE;
 
   QuantParams qp;
   memset(&qp, 0, sizeof(qp));
   qp.v = static_cast<const char*>(a->v);
   qp.dst = static_cast<char*>(a->v_dst);
   qp.scale = a->v_scale;
+  qp.partial = partial;
   for (int i = 0; i < 3; ++i) {
     qp.sv[i] = a->stride_v[i];
     qp.sd[i] = a->stride_v_dst[i];
@@ -484,20 +534,66 @@ int qik_slab_store(const qik_slab_store_args* a, void* stream) {
   qp.P = (int)a->P;
   qp.H = (int)a->H;
   // spread the heads over the device: about two workgroups per CU in total,
-  // at least 32 rows per workgroup, at most 64 workgroups per head
+  // at least 32 rows per workgroup, at most MAX_SCALE_CHUNKS per head
   const int64_t heads = a->B * a->H;
-  if (heads > (int64_t)(UINT_MAX / 64)) return QIK_ERR_SHAPE;
   const int cus = device_cus();
   int64_t chunks = cus > 0 ? 2 * cus / heads : 1;
-  chunks = std::max<int64_t>(1, std::min<int64_t>({chunks, 64, a->P / 32}));
+  chunks = std::max<int64_t>(1, std::min<int64_t>({chunks, (int64_t)MAX_SCALE_CHUNKS, a->P / 32}));
   qp.chunks = (int)chunks;
   void* qargs[] = {&qp};
+  const void* fq = a->D == 128 ? (const void*)slab_quant_fp8_kernel<128> : (const void*)slab_quant_fp8_kernel<64>;
+
+  if (fp8 && partial != nullptr) {
+    // K copy and the chunks' scales in one launch, then the codes
+    const int64_t ncopy = (threads + QTHREADS - 1) / QTHREADS;
+    if (ncopy + heads * chunks > (int64_t)INT_MAX) return QIK_ERR_SHAPE;
+    int nc = (int)ncopy;
+    void* args2[] = {&cp, &qp, &nc};
+    const void* fc = a->D == 128 ? (const void*)slab_copy_scale_kernel<128> : (const void*)slab_copy_scale_kernel<64>;
+    if (hipLaunchKernel(fc, dim3((unsigned)(ncopy + heads * chunks)), dim3(QTHREADS), args2, 0, s) != hipSuccess)
+      return QIK_ERR_LAUNCH;
+    return hipLaunchKernel(fq, dim3((unsigned)(heads * chunks)), dim3(QTHREADS), qargs, 0, s) == hipSuccess
+               ? QIK_OK : QIK_ERR_LAUNCH;
+  }
+
+  void* cargs[] = {&cp};
+  hipError_t e = hipLaunchKernel(reinterpret_cast<const void*>(slab_copy_kernel), dim3((unsigned)grid, fp8 ? 1 : 2),
+                                 dim3(NTHREADS), cargs, 0, s);
+  if (e != hipSuccess) return QIK_ERR_LAUNCH;
+  if (!fp8) return QIK_OK;
   const void* fs = a->D == 128 ? (const void*)slab_scale_fp8_kernel<128> : (const void*)slab_scale_fp8_kernel<64>;
   e = hipLaunchKernel(fs, dim3((unsigned)(heads * chunks)), dim3(QTHREADS), qargs, 0, s);
   if (e != hipSuccess) return QIK_ERR_LAUNCH;
-  const void* fq = a->D == 128 ? (const void*)slab_quant_fp8_kernel<128> : (const void*)slab_quant_fp8_kernel<64>;
   e = hipLaunchKernel(fq, dim3((unsigned)(heads * chunks)), dim3(QTHREADS), qargs, 0, s);
   return e == hipSuccess ? QIK_OK : QIK_ERR_LAUNCH;
+}
+
+}  // namespace qik_ops
+
+extern "C" {
+
+int qik_slab_store(const qik_slab_store_args* a, void* stream) {
+  return qik_ops::store(a, nullptr, static_cast<hipStream_t>(stream));
+}
+
+int qik_slab_store_workspace_size(const qik_slab_store_args* a, int64_t* bytes) {
+  if (bytes == nullptr) return QIK_ERR_NULL_ARG;
+  *bytes = 0;
+  int64_t rows = 0;
+  const int st = qik_ops::validate_store(a, &rows);
+  if (st != QIK_OK) return st;
+  if (a->v_fp8 != 0) *bytes = a->B * a->H * qik_ops::MAX_SCALE_CHUNKS * (int64_t)sizeof(float);
+  return QIK_OK;
+}
+
+int qik_slab_store_ws(const qik_slab_store_args* a, void* workspace, int64_t workspace_bytes, void* stream) {
+  int64_t rows = 0;
+  const int st = qik_ops::validate_store(a, &rows);
+  if (st != QIK_OK || rows == 0) return st;
+  if (a->v_fp8 == 0) return qik_ops::store(a, nullptr, static_cast<hipStream_t>(stream));
+  const int64_t need = a->B * a->H * qik_ops::MAX_SCALE_CHUNKS * (int64_t)sizeof(float);
+  if (workspace == nullptr || workspace_bytes < need || !qik_ops::aligned_to(workspace, 4)) return QIK_ERR_WORKSPACE;
+  return qik_ops::store(a, static_cast<float*>(workspace), static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

@@ -8,11 +8,12 @@ head's prefix tokens are dense (256 B rows of bf16 K, 128 B rows of fp8 V), and
 ``views()`` returns ``[B, P, H, D]`` strided views that the attention kernel
 reads in place.
 
-``store`` on a HIP device is one call of ``qik_slab_store`` (include/qik_ops.h):
+``store`` on a HIP device is one call of ``qik_slab_store_ws`` (include/qik_ops.h):
 the transposed copy of K (and of a bf16 V) and, for an fp8 slab, the per-(b, h)
 amax, scale and e4m3fn codes of V, bit-identical to the torch ops of
-kv_cache.py:36-42 run on the same device.  A slab on the CPU (the reference's
-own CPU-runnable case) runs those torch ops.
+kv_cache.py:36-42 run on the same device, in two launches with a small
+workspace that the cache keeps per (device, stream).  A slab on the CPU (the
+reference's own CPU-runnable case) runs those torch ops.
 
 Difference from the reference: the prefix length of each layer is also kept on
 the host, so ``get()``/``views()`` do not synchronise the device
@@ -58,9 +59,15 @@ class _LayerView:
     def _store_device(self, k: torch.Tensor, v: torch.Tensor, P: int) -> None:
         a, keep = self.store_args(k, v, P)
         kd = self._c.k_buf
+        lib = _lib.load()
         with torch.cuda.device(kd.device):
-            stream = torch.cuda.current_stream(kd.device).cuda_stream
-            _lib.check(_lib.load().qik_slab_store(ctypes.byref(a), stream), "qik_slab_store")
+            stream = torch.cuda.current_stream(kd.device)
+            nbytes = ctypes.c_int64(0)
+            _lib.check(lib.qik_slab_store_workspace_size(ctypes.byref(a), ctypes.byref(nbytes)),
+                       "qik_slab_store_workspace_size")
+            ws = self._c._workspace(stream, nbytes.value)
+            _lib.check(lib.qik_slab_store_ws(ctypes.byref(a), ws, nbytes.value, stream.cuda_stream),
+                       "qik_slab_store_ws")
         del keep
 
     def store_args(self, k: torch.Tensor, v: torch.Tensor, P: int):
@@ -152,7 +159,23 @@ class ContiguousKVCache:
         self.v_scale = torch.empty(num_layers, batch, num_heads, dtype=torch.float32, device=device)
         self.lengths = torch.zeros(num_layers, dtype=torch.int64, device=device)
         self._host_lengths = [0] * num_layers
+        self._ws: dict = {}   # (device index, stream) -> store workspace (fp8 slab)
         self.layers = [_LayerView(self, i) for i in range(num_layers)]
+
+    def _workspace(self, stream, nbytes: int):
+        """Device pointer of this cache's store workspace for `stream` (None when none is needed).
+
+        Its contents never need clearing: every store writes what it reads.
+        Stores on different streams get different workspaces.
+        """
+        if nbytes <= 0:
+            return None
+        key = (stream.device.index, stream.cuda_stream)
+        ws = self._ws.get(key)
+        if ws is None or ws.numel() < nbytes:
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=stream.device)
+            self._ws[key] = ws
+        return ws.data_ptr()
 
     def get_layer(self, i: int) -> _LayerView:
         return self.layers[i]

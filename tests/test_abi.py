@@ -255,3 +255,33 @@ def test_slab_store_rejects_before_any_device_call(kw, code):
 
 def test_slab_store_without_rows_is_a_no_op():
     assert _lib.load().qik_slab_store(ctypes.byref(_store_args(P=0, k=None)), None) == 0
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(abi_version=0), -2), (dict(dtype=9), -3), (dict(D=32), -4), (dict(P=-1), -5),
+    (dict(v_scale=None), -7), (dict(dtype=_lib.DTYPE_FP16), -7),
+    (dict(k=None), -1), (dict(v_dst=0x10004), -8),
+])
+def test_slab_store_ws_rejects_like_the_three_launch_store(kw, code):
+    lib = _lib.load()
+    ws = (ctypes.c_float * (2 * 64))()
+    assert lib.qik_slab_store_ws(ctypes.byref(_store_args(**kw)), ctypes.addressof(ws), 2 * 64 * 4, None) == code
+
+
+def test_slab_store_workspace_checks_and_size():
+    """fp8 V: B*H*64 fp32 partial scales, 4-byte aligned; no workspace needed otherwise."""
+    lib = _lib.load()
+    n = ctypes.c_int64(-1)
+    assert lib.qik_slab_store_workspace_size(ctypes.byref(_store_args()), ctypes.byref(n)) == 0
+    assert n.value == 1 * 2 * 64 * 4
+    assert lib.qik_slab_store_workspace_size(ctypes.byref(_store_args(v_fp8=0, v_scale=None)), ctypes.byref(n)) == 0
+    assert n.value == 0
+    assert lib.qik_slab_store_workspace_size(ctypes.byref(_store_args()), None) == -1
+    buf = (ctypes.c_float * 256)()
+    base = ctypes.addressof(buf)
+    WS = -12
+    assert lib.qik_slab_store_ws(ctypes.byref(_store_args()), None, 512, None) == WS
+    assert lib.qik_slab_store_ws(ctypes.byref(_store_args()), base, 511, None) == WS
+    assert lib.qik_slab_store_ws(ctypes.byref(_store_args()), base + 2, 512, None) == WS
+    # no rows: nothing to do, no workspace looked at
+    assert lib.qik_slab_store_ws(ctypes.byref(_store_args(P=0, k=None)), None, 0, None) == 0

@@ -11,6 +11,8 @@
   the stock composition: torch RMSNorm + RoPE, fp32 explicit-mask attention.
 """
 
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -21,6 +23,7 @@ from oracle import lengths as ol
 from oracle import rms_rope as orr
 
 import qwen_image_kernel_amd as qik
+from qwen_image_kernel_amd import _lib
 
 pytestmark = pytest.mark.gpu
 
@@ -129,6 +132,38 @@ def test_slab_store_bit_exact_vs_torch_ops(B, P, H, D, v_fp8):
     assert cache.lengths[2].item() == P and cache._host_lengths[2] == P
     # the other layers are untouched
     assert cache.lengths[0].item() == 0
+
+
+@pytest.mark.parametrize("B,P,H,D", [(1, 2560, 24, 128), (2, 333, 5, 128), (1, 100, 3, 64), (3, 31, 2, 128)])
+def test_slab_store_two_and_three_launch_forms_agree(B, P, H, D):
+    """qik_slab_store_ws (workspace of chunk scales, two launches) against
+    qik_slab_store (atomic scale, three launches): the same bytes, with a reused
+    workspace holding the previous call's (or garbage) values."""
+    _flush(f"case slab store forms B={B} P={P} H={H} D={D}")
+    lib = _lib.load()
+    g = torch.Generator().manual_seed(900 + P)
+    k = torch.randn(B, P, H, D, generator=g).to(torch.bfloat16).to(DEV)
+    v = (torch.randn(B, P, H, D, generator=g) * 5).to(torch.bfloat16).to(DEV)
+    caches = [qik.ContiguousKVCache(1, B, P + 16, H, D, v_fp8=True, device=DEV) for _ in range(2)]
+    stream = torch.cuda.current_stream().cuda_stream
+    a3, keep3 = caches[0].get_layer(0).store_args(k, v, P)
+    assert lib.qik_slab_store(ctypes.byref(a3), stream) == 0
+    a2, keep2 = caches[1].get_layer(0).store_args(k, v, P)
+    n = ctypes.c_int64()
+    assert lib.qik_slab_store_workspace_size(ctypes.byref(a2), ctypes.byref(n)) == 0
+    ws = torch.full((n.value // 4,), 1e30, dtype=torch.float32, device=DEV)     # garbage in the workspace
+    for _ in range(2):
+        assert lib.qik_slab_store_ws(ctypes.byref(a2), ws.data_ptr(), n.value, stream) == 0
+    torch.cuda.synchronize()
+    for buf in ("k_buf", "v_buf", "v_scale"):
+        x, y = getattr(caches[0], buf), getattr(caches[1], buf)
+        if buf == "k_buf":
+            x, y = x[..., :P, :], y[..., :P, :]
+        elif buf == "v_buf":
+            x, y = x[..., :P, :].contiguous().view(torch.uint8), y[..., :P, :].contiguous().view(torch.uint8)
+        np.testing.assert_array_equal(_bits(x) if buf == "k_buf" else x.cpu().numpy(),
+                                      _bits(y) if buf == "k_buf" else y.cpu().numpy(), err_msg=buf)
+    del keep3, keep2
 
 
 def test_slab_store_rounding_edges():
