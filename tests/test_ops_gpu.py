@@ -59,6 +59,8 @@ def _rope_oracle(x, w, freqs, eps, dtype="bf16"):
     (2, 77, 24, 128, torch.bfloat16),
     (1, 130, 5, 64, torch.bfloat16),
     (1, 65, 3, 128, torch.float16),
+    (2, 9, 1, 128, torch.bfloat16),      # one head: a thread's next row is 16 positions on
+    (4, 3, 2, 128, torch.bfloat16),      # 16 rows on crosses whole batches (b carry)
 ])
 def test_rms_rope_bit_exact_vs_oracle(B, S, H, D, dtype):
     _flush(f"case rms_rope {B}x{S}x{H}x{D} {dtype}")
