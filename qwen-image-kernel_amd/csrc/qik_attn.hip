@@ -20,12 +20,15 @@
 //     the V^T A-operand comes straight from the row-major V tile in LDS through
 //     ds_read_b64_tr_b16 (the gfx950 LDS transpose read).
 //   * K and V tiles (BN=64 keys) are double-buffered in LDS with a 16-byte
-//     chunk swizzle (swz below); the fp8 slab V is dequantised to bf16 once per workgroup
-//     while it is written to LDS.
+//     chunk swizzle (swz below), copied global -> LDS directly (buffer_load
+//     ... lds, issued as asm); the fp8 slab V goes through registers and is
+//     dequantised to bf16 once per workgroup while it is written to LDS.
 //   * Whole KV tiles past the row block's largest L are never visited; tiles
-//     that are entirely allowed for a wave skip the mask arithmetic.
-//   * blockIdx is remapped so that one (b, h)'s row blocks share an XCD (and
-//     its L2), heaviest row blocks first.
+//     that are entirely allowed for a wave (and, with key_valid, whose keys
+//     are all valid) skip the mask arithmetic.
+//   * Row blocks reach workgroups through per-XCD queues (qik_plan.h): one
+//     (b, h)'s row blocks share an XCD and its L2, heaviest first, and with a
+//     workspace the last partial round runs as two pieces per row block.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
