@@ -6,7 +6,9 @@
  *                   (replaces `fused_rms_norm_rope`, qwen_image_kernel/triton_fused.py:75-105)
  *   qik_slab_store  writes one layer's prefix K/V into the contiguous slab,
  *                   quantising V to fp8e4m3fn per (b, h)
- *                   (replaces `_LayerView.store`, qwen_image_kernel/kv_cache.py:30-45)
+ *                   (replaces `_LayerView.store`, qwen_image_kernel/kv_cache.py:30-45);
+ *                   qik_slab_store_ws is the same store in fewer launches with a
+ *                   small caller workspace
  *
  * Same conventions as qik_attn.h: plain C, no allocation, device pointers of
  * the current HIP device, `stream` a hipStream_t as void*, asynchronous and

@@ -251,13 +251,17 @@ __global__ void __launch_bounds__(NTHREADS) slab_copy_kernel(const CopyParams p)
   copy_chunk(p, which, g);
 }
 
-// fp8 V in two launches over `chunks` workgroups per (b, h), workgroup c
-// owning rows [c*P/chunks, (c+1)*P/chunks) of the head:
-//   slab_scale_fp8_kernel: scale of its rows, max(amax * fp32(1/448), 1e-12),
-//     atomically maxed into scale[b*H + h] (zeroed by the copy launch before).
-//     The map amax -> scale is monotone (fp32 rounding included), so the max of
-//     the rows' scales is the scale of the head's amax;
-//   slab_quant_fp8_kernel: the codes of its rows with the head's scale.
+// fp8 V over `chunks` workgroups per (b, h), workgroup c owning rows
+// [c*P/chunks, (c+1)*P/chunks) of the head.  The scale of a chunk's rows is
+// max(amax * fp32(1/448), 1e-12); the map amax -> scale is monotone (fp32
+// rounding included), so the largest chunk scale is the scale of the head's
+// amax.  Two forms:
+//   qik_slab_store: slab_scale_fp8_kernel maxes each chunk's scale atomically
+//     into scale[b*H + h] (zeroed by the copy launch before), then
+//     slab_quant_fp8_kernel writes the codes (three launches with the copy);
+//   qik_slab_store_ws: slab_copy_scale_kernel copies K and writes each chunk's
+//     scale into the workspace, then slab_quant_fp8_kernel takes the largest of
+//     its head's and writes the codes and the scale (two launches).
 struct QuantParams {
   const char* v;     // bf16 [B, P, H, D]
   char* dst;         // fp8 slab V of the layer
