@@ -85,7 +85,8 @@ struct Params {
 
 // A split item with fewer than SPLIT_MIN_TILES KV tiles runs whole (its
 // second piece is skipped).  Otherwise piece 0 takes its first
-// (7 T + 5) / 10 tiles and piece 1 the rest.
+// (7 T + 5) / 10 tiles (half of them, (T + 1) / 2, when the plan says `even`)
+// and piece 1 the rest.
 constexpr int SPLIT_MIN_TILES = 16;
 
 // Partial softmax state of one thread of a split piece: its DBLK x 16 fp32
@@ -353,7 +354,7 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params args
     // pieces (T, and so the split, is the same for both pieces of the item)
     const bool split = wk.group >= 0 && T >= SPLIT_MIN_TILES;
     if (wk.piece > 0 && !split) continue;
-    const int gsplit = (7 * T + 5) / 10;
+    const int gsplit = p.plan.even ? (T + 1) / 2 : (7 * T + 5) / 10;
     const int g0 = (split && wk.piece) ? gsplit : 0;
     const int g1 = (split && !wk.piece) ? gsplit : T;
 

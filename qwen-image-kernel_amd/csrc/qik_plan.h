@@ -18,7 +18,10 @@
 // free up in two waves: the first takes the big pieces, the second the small
 // ones, and both finish about together (measured on MI355X: 0.6 to 0.75 of
 // the tiles for the big piece are all within 1%), where equal halves leave
-// the early slot idle while the late one finishes.  The two pieces of an item combine
+// the early slot idle while the late one finishes.  When an XCD has no whole
+// round and every piece gets a slot of its own (a launch smaller than the
+// device), all pieces start together and the launch lasts as long as the
+// biggest: then the pieces are equal halves.  The two pieces of an item combine
 // their partial softmax states through the workspace slots of its group.
 //
 // plan_work(pl, loc * NXCD + x) is the unit at queue position loc of XCD x;
@@ -47,6 +50,7 @@ struct WorkPlan {
   int wpx;               // workgroups per XCD; grid = NXCD * wpx
   int mb_major;          // 1: an XCD's items are whole heads, walked rank-major
   int ngroups;           // split items (workspace slot groups of ns slots)
+  int even;              // 1: the two pieces are equal halves, else 7/10 and 3/10
 };
 
 struct Work {
@@ -86,6 +90,7 @@ inline WorkPlan make_plan(int n, int nmb, int sx, int split, int ragged = 1) {
   const int w_hi = pl.rem > 0 ? pl.full_hi + pl.ns * r_hi : 0;
   pl.wpx = w_lo > w_hi ? w_lo : w_hi;
   pl.ngroups = pl.rem * r_hi + (NXCD - pl.rem) * r_lo;
+  pl.even = (pl.ns > 1 && pl.full_lo == 0 && pl.full_hi == 0 && pl.wpx <= sx) ? 1 : 0;
   pl.mb_major = (split && ragged && pl.rem == 0 && nmb > 0 && pl.per % nmb == 0) ? 1 : 0;
   return pl;
 }
