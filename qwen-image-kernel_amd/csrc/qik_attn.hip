@@ -294,13 +294,24 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params args
   // ---- units: without a workspace this workgroup's one unit; with one, the
   // units of this XCD's queue until it runs dry (qik_plan.h).  Nothing waits
   // on another workgroup: a workgroup that is not resident yet simply starts
-  // later and finds the queue further on.
+  // later and finds the queue further on.  The gx workgroups of an XCD take
+  // positions 0 .. gx-1 in blockIdx order (all of them drawing from the one
+  // counter at the start of the launch queued behind each other); later
+  // positions come from the counter, drawn at the end of a unit's tile loop so
+  // that the atomic's round trip overlaps the unit's merge and store.
   const bool pulled = args.ctl != nullptr;
   const int xcd = (int)(blockIdx.x % NXCD);
+  const int gx = (int)(gridDim.x / NXCD);
+  int pend = -1;  // thread 0: the position drawn at the end of the last tile loop
   for (int first = 1;; first = 0) {
     int bidv = (int)blockIdx.x;
     if (pulled) {
-      if (tid == 0) snext = (int)__hip_atomic_fetch_add(args.ctl + xcd, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (tid == 0) {
+        snext = pend >= 0 ? pend
+              : first ? (int)(blockIdx.x / NXCD)
+                      : gx + (int)__hip_atomic_fetch_add(args.ctl + xcd, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      pend = -1;
       __syncthreads();
       const int loc = snext;
       __syncthreads();  // every thread has read snext before the next unit's head rewrites it
@@ -638,6 +649,7 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params args
     // can hold an older copy; the pieces of an item come from one XCD's queue,
     // so the lines are normally still in that XCD's L2.
     const Params pe = reread_args();
+    if (pulled && tid == 0) pend = gx + (int)__hip_atomic_fetch_add(pe.ctl + xcd, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     float l_part = l_run;
     if (split) {
       constexpr int OB = slot_oacc_bytes<D>();
