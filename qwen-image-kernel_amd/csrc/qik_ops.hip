@@ -303,15 +303,19 @@ __device__ __forceinline__ float chunk_scale(const QuantParams& p, const int bx)
       amax = fmaxf(amax, fabsf(__uint_as_float(w[i] & 0xffff0000u)));
     }
   };
-  int pp = p0 + r0;
-  for (; pp + (U - 1) * RPS < p1; pp += U * RPS) {
+  // U rows per batch, all loads issued before the first is used; rows past
+  // the chunk are skipped (a chunk is a few batches, so a batch is never
+  // broken into one-row steps that would each wait for their load)
+  for (int pp = p0 + r0; pp < p1; pp += U * RPS) {
     u32x4 raw[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) raw[u] = *reinterpret_cast<const u32x4*>(src + (pp + u * RPS) * rs);
+    for (int u = 0; u < U; ++u) {
+      raw[u] = u32x4{0u, 0u, 0u, 0u};
+      if (pp + u * RPS < p1) raw[u] = *reinterpret_cast<const u32x4*>(src + (pp + u * RPS) * rs);
+    }
 #pragma unroll
     for (int u = 0; u < U; ++u) absmax8(raw[u]);
   }
-  for (; pp < p1; pp += RPS) absmax8(*reinterpret_cast<const u32x4*>(src + pp * rs));
 #pragma unroll
   for (int k = 32; k >= 1; k >>= 1) amax = fmaxf(amax, __shfl_xor(amax, k));
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
@@ -363,6 +367,19 @@ __global__ void __launch_bounds__(QTHREADS) slab_quant_fp8_kernel(const QuantPar
   const int64_t rs = p.sv[1] * 2;
   const int p0 = (int)((int64_t)p.P * c / p.chunks);
   const int p1 = (int)((int64_t)p.P * (c + 1) / p.chunks);
+  // U rows per batch, all loads issued before the first is used; the first
+  // batch is in flight while the head's scale is formed
+  constexpr int U = 4;
+  u32x4 raw[U];
+  auto load_batch = [&](const int q0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      raw[u] = u32x4{0u, 0u, 0u, 0u};
+      if (q0 + u * RPS < p1) raw[u] = *reinterpret_cast<const u32x4*>(src + (q0 + u * RPS) * rs);
+    }
+  };
+  int q0 = p0 + r0;
+  load_batch(q0);
   float scale;
   if (p.partial != nullptr) {
     // the head's scale is the largest of its chunks' (amax -> scale is
@@ -374,22 +391,28 @@ __global__ void __launch_bounds__(QTHREADS) slab_quant_fp8_kernel(const QuantPar
     scale = p.scale[bh];
   }
   char* dst = p.dst + b * p.sd[0] + h * p.sd[1] + t * 8;
-  for (int q0 = p0 + r0; q0 < p1; q0 += RPS) {
-    const u32x4 raw = *reinterpret_cast<const u32x4*>(src + q0 * rs);
-    const unsigned w[4] = {raw.x, raw.y, raw.z, raw.w};
-    // v / scale (IEEE division), clamped to the e4m3fn range, rounded to
-    // nearest even by the hardware conversion; byte k of the 8 = element 8t+k
-    float q[8];
+  for (;;) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      q[2 * i] = fminf(fmaxf(__uint_as_float(w[i] << 16) / scale, -448.0f), 448.0f);
-      q[2 * i + 1] = fminf(fmaxf(__uint_as_float(w[i] & 0xffff0000u) / scale, -448.0f), 448.0f);
+    for (int u = 0; u < U; ++u) {
+      if (q0 + u * RPS >= p1) continue;
+      const unsigned w[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
+      // v / scale (IEEE division), clamped to the e4m3fn range, rounded to
+      // nearest even by the hardware conversion; byte k of the 8 = element 8t+k
+      float q[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        q[2 * i] = fminf(fmaxf(__uint_as_float(w[i] << 16) / scale, -448.0f), 448.0f);
+        q[2 * i + 1] = fminf(fmaxf(__uint_as_float(w[i] & 0xffff0000u) / scale, -448.0f), 448.0f);
+      }
+      int lo = __builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
+      lo = __builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], lo, true);
+      int hi = __builtin_amdgcn_cvt_pk_fp8_f32(q[4], q[5], 0, false);
+      hi = __builtin_amdgcn_cvt_pk_fp8_f32(q[6], q[7], hi, true);
+      *reinterpret_cast<u32x2*>(dst + (q0 + u * RPS) * p.sd[2]) = u32x2{(unsigned)lo, (unsigned)hi};
     }
-    int lo = __builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
-    lo = __builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], lo, true);
-    int hi = __builtin_amdgcn_cvt_pk_fp8_f32(q[4], q[5], 0, false);
-    hi = __builtin_amdgcn_cvt_pk_fp8_f32(q[6], q[7], hi, true);
-    *reinterpret_cast<u32x2*>(dst + q0 * p.sd[2]) = u32x2{(unsigned)lo, (unsigned)hi};
+    q0 += U * RPS;
+    if (q0 >= p1) break;
+    load_batch(q0);
   }
 }
 
