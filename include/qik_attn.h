@@ -116,8 +116,9 @@ int qik_attn_fwd(const qik_attn_args* args, void* stream);
  * words (queue heads, exit and arrival counts) and the partial softmax states
  * of split row blocks: the launch runs whole rounds of row blocks, then splits
  * each row block of the last, partly filled round over its KV tiles into two
- * pieces (seven tenths and three tenths of its tiles) that the second to finish
- * combines.  The size depends on the shape and on the device's CU count only,
+ * pieces (seven tenths and three tenths of its tiles; halves when the launch
+ * has no whole round and every piece gets a workgroup of its own) that the
+ * second to finish combines.  The size depends on the shape and on the device's CU count only,
  * stays below 2 x (workgroups resident at once) x (BM x D x 4 + 2 KiB)
  * + 32 KiB (about 70 MB on MI355X, D = 128), and is about 41 MB for
  * Qwen-Image's 24-head, 4352-row layer.  Host-only (a cached device-attribute
