@@ -185,6 +185,28 @@ def test_first_row_and_empty_rows_exact():
     _check(out, ref, what="known answers")
 
 
+def test_empty_query_and_no_fresh_keys():
+    """Zero query rows return an empty output without a launch (the reference's grid is
+    empty); with no fresh keys (SN = 0) the rows attend the slab alone."""
+    _flush("case empty query / no fresh keys")
+    g = torch.Generator().manual_seed(31)
+    k, v = _rand((1, 64, 2, 128), g), _rand((1, 64, 2, 128), g)
+    q0 = torch.empty(1, 0, 2, 128, dtype=torch.bfloat16, device=DEV)
+    out0 = qik.block_causal_flash_attention(q0, k.to(DEV), v.to(DEV), torch.empty(0, dtype=torch.int32, device=DEV),
+                                            None)
+    assert out0.shape == q0.shape
+    B, P, H, D, SQ = 2, 200, 3, 128, 96
+    q, kn, vn, ck, cv, cache = _slab_case(B, P, 0, SQ, H, D, 700)
+    k8, v8, sc = cache.get_layer(1).views()
+    rng = np.random.default_rng(31)
+    L = rng.integers(-1, P, size=SQ).astype(np.int32)
+    for split in (True, False):
+        out = qik.block_causal_flash_attention(q.to(DEV), kn.to(DEV), vn.to(DEV), torch.from_numpy(L).to(DEV), None,
+                                               cache_k=k8, cache_v=v8, cache_v_scale=sc, split_tail=split)
+        ref = oa.attention_fp32(q, kn, vn, L, None, k8.cpu(), v8.cpu(), sc.cpu())
+        _check(out, ref, what=f"slab only, split={split}")
+
+
 def test_all_keys_invalid_gives_zeros():
     g = torch.Generator().manual_seed(710)
     q, k, v = (_rand((1, 96, 2, 128), g) for _ in range(3))
