@@ -53,7 +53,9 @@ class _LayerView:
             self._store_device(k, v, P)
         else:
             self._store_torch(k, v, P)
-        c.lengths[self._layer] = P
+        # a fill kernel: assigning a Python int to one element is a host-to-device
+        # copy, which a stream under graph capture rejects
+        c.lengths[self._layer:self._layer + 1].fill_(P)
         c._host_lengths[self._layer] = P
 
     def _store_device(self, k: torch.Tensor, v: torch.Tensor, P: int) -> None:
