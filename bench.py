@@ -190,7 +190,9 @@ def clock_under_load(calls, dev, seconds: float = 1.5) -> dict:
     Runs after the timed region: the step's launches are repeated for about
     ``seconds`` while a host thread samples the device's sysfs ``pp_dpm_sclk``
     (and board power) every 20 ms, and ``amd-smi metric --clock`` is run once
-    as a child process for the per-XCD GFX clocks.  Every source is optional.
+    as a child process for the per-XCD GFX clocks; the launches continue until
+    it returns (at most 25 s more), so that it reads the clocks under load.
+    Every source is optional.
     """
     import re
     import subprocess
@@ -198,7 +200,7 @@ def clock_under_load(calls, dev, seconds: float = 1.5) -> dict:
 
     import torch
 
-    out: dict = {"when": f"{seconds} s of the same launches right after the timed region"}
+    out: dict = {"when": f"{seconds} s (longer while amd-smi runs) of the same launches right after the timed region"}
     ddir = _sysfs_device_dir(dev)
     samples, power = [], []
     stop = threading.Event()
@@ -219,10 +221,18 @@ def clock_under_load(calls, dev, seconds: float = 1.5) -> dict:
     th = threading.Thread(target=sampler, daemon=True) if ddir else None
     smi: dict = {}
 
+    # this device only: amd-smi lists every GPU of the host, ours by its PCI address
+    props = torch.cuda.get_device_properties(dev)
+    bdf = f"{props.pci_domain_id:04x}:{props.pci_bus_id:02x}:{props.pci_device_id:02x}.0"
+    out["amd_smi_gpu"] = bdf
+
     def run_smi():
         try:
-            r = subprocess.run(["amd-smi", "metric", "--clock"], capture_output=True, text=True, timeout=20)
+            r = subprocess.run(["amd-smi", "metric", "--gpu", bdf, "--clock"], capture_output=True, text=True,
+                               timeout=20)
             smi["text"] = r.stdout
+            if r.returncode != 0:
+                smi["error"] = f"exit {r.returncode}: {r.stderr.strip()[:200]}"
         except (OSError, subprocess.SubprocessError) as e:
             smi["error"] = type(e).__name__
 
@@ -231,13 +241,21 @@ def clock_under_load(calls, dev, seconds: float = 1.5) -> dict:
         th.start()
     t0 = time.perf_counter()
     started = False
-    while time.perf_counter() - t0 < seconds:
+    # the launches go on until amd-smi has returned (it takes a second or more
+    # to start): read after the load, its clocks are the idle ones
+    while True:
+        el = time.perf_counter() - t0
+        if el >= seconds and not (started and sm.is_alive()):
+            break
+        if el >= seconds + 25.0:
+            break
         for _, fn in calls:
             fn()
-        if not started and time.perf_counter() - t0 > 0.3:
+        if not started and el > 0.3:
             sm.start()
             started = True
         torch.cuda.synchronize()
+    out["amd_smi_under_load"] = started and not sm.is_alive()
     stop.set()
     if th:
         th.join()
@@ -253,7 +271,7 @@ def clock_under_load(calls, dev, seconds: float = 1.5) -> dict:
     gfx = [float(x) for x in re.findall(r"GFX_\d+:\s*\n\s*CLK:\s*([\d.]+)\s*MHz", smi.get("text", ""))]
     if gfx:
         out["amd_smi_gfx_clk_mhz"] = gfx
-    elif "error" in smi:
+    if "error" in smi:
         out["amd_smi"] = smi["error"]
     return out
 
