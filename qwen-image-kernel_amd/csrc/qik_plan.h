@@ -47,7 +47,9 @@ struct WorkPlan {
   int per, rem;          // items per XCD: per + 1 on XCDs x < rem, per on the others
   int full_lo, full_hi;  // items an XCD runs whole when it has per / per + 1 items
   int ns;                // pieces per split item (1: nothing is split)
-  int wpx;               // workgroups per XCD; grid = NXCD * wpx
+  int wpx;               // positions per XCD: the workgroups of a launch without a
+                         // workspace (grid NXCD * wpx), or the queue length of one
+                         // with (grid NXCD * min(sx, wpx))
   int mb_major;          // 1: an XCD's items are whole heads, walked rank-major
   int ngroups;           // split items (workspace slot groups of ns slots)
   int even;              // 1: the two pieces are equal halves, else 7/10 and 3/10
