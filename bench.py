@@ -53,6 +53,9 @@ def parse():
                          "launches (0 disables it)")
     ap.add_argument("--only", choices=["t2i_1024", "edit_768"], default=None,
                     help="time one shape only (profiling aid; the default times both)")
+    ap.add_argument("--all-workloads", action="store_true",
+                    help="instead of the benchmark, time every workload of the benchmark set (t2i_512, "
+                         "t2i_1024, edit_768, multiref_cfg), print one JSON line and exit")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="instead of the benchmark, run 5 plain device copies of this many MiB "
                          "(reference point for the FETCH_SIZE / WRITE_SIZE counters) and exit")
@@ -69,6 +72,69 @@ def copy_calibration(mb: int) -> None:
         dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"copy_calibration_bytes_per_copy": n * 4, "copies": 5}), flush=True)
+
+
+def all_workloads() -> None:
+    """Kernel time of every workload of the benchmark set through qik_attn_fwd_ws.
+
+    Per workload: 8 independent layers launched back to back (multiref_cfg:
+    4), 3 warm-up passes, then 5 groups of 4 passes with HIP events around
+    each group; the median group gives the time per launch.
+    """
+    import ctypes
+
+    import torch
+
+    import qwen_image_kernel_amd.workloads as wls
+    from qwen_image_kernel_amd import _lib
+    from qwen_image_kernel_amd.attention import make_args
+
+    lib = _lib.load()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    res, runs = {}, []
+    for name in ("t2i_512", "t2i_1024", "edit_768", "multiref_cfg"):
+        wl = wls.workload(name)
+        nl = 4 if name == "multiref_cfg" else 8
+        layers = [wls.make_inputs(wl, seed=40 + i, device="cuda", gen_device="cuda") for i in range(nl)]
+        calls = []
+        for inp in layers:
+            out = torch.empty_like(inp["query"])
+            L = None if wl.uniform else inp["prefix_lengths"]
+            a = make_args(inp["query"], inp["key"], inp["value"], L, None, out, inp["cache_k"], inp["cache_v"],
+                          inp["cache_v_scale"], wl.uniform)
+            nb = ctypes.c_int64()
+            _lib.check(lib.qik_attn_workspace_size(ctypes.byref(a), ctypes.byref(nb)), "qik_attn_workspace_size")
+            ws = torch.zeros(max(nb.value, 256), dtype=torch.uint8, device=dev)
+            calls.append((a, ws, nb.value, out))
+
+        def run(calls=calls):
+            for a, ws, nb, _ in calls:
+                _lib.check(lib.qik_attn_fwd_ws(ctypes.byref(a), ws.data_ptr(), nb, stream), "qik_attn_fwd_ws")
+
+        for _ in range(3):
+            run()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(5):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(4):
+                run()
+            e1.record()
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1) * 1e3 / (4 * len(calls)))
+        us = sorted(ts)[len(ts) // 2]
+        tf = wl.flops() / us / 1e6
+        res[name] = {"us_per_launch": round(us, 2), "tflops": round(tf, 1),
+                     "pct_bf16_peak": round(100 * tf / PEAK_BF16_TFLOPS, 2), "layers": nl,
+                     "shape": [wl.B, wl.SQ, wl.H, wl.D], "P": wl.P, "SN": wl.SN,
+                     "unmasked_gflop": round(wl.flops() / 1e9, 3)}
+        print(name, json.dumps(res[name]), file=sys.stderr, flush=True)
+        if name in ("t2i_1024", "edit_768"):
+            runs.append((name, run))
+    print(json.dumps({"all_workloads": res, "gpu_clock": clock_under_load(runs, dev, 1.5)}), flush=True)
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "attn_fwd_traffic.txt")
@@ -189,18 +255,15 @@ def clock_under_load(calls, dev, seconds: float = 1.5) -> dict:
 
     Runs after the timed region: the step's launches are repeated for about
     ``seconds`` while a host thread samples the device's sysfs ``pp_dpm_sclk``
-    (and board power) every 20 ms, and ``amd-smi metric --clock`` is run once
-    as a child process for the per-XCD GFX clocks; the launches continue until
-    it returns (at most 25 s more), so that it reads the clocks under load.
-    Every source is optional.
+    (and board power) every 20 ms.  Every source is optional.  (amd-smi's
+    per-XCD clock readings were tried here and dropped: one snapshot of them
+    read anywhere from the sysfs median down to a tenth of it.)
     """
-    import re
-    import subprocess
     import threading
 
     import torch
 
-    out: dict = {"when": f"{seconds} s (longer while amd-smi runs) of the same launches right after the timed region"}
+    out: dict = {"when": f"{seconds} s of the same launches right after the timed region"}
     ddir = _sysfs_device_dir(dev)
     samples, power = [], []
     stop = threading.Event()
@@ -219,48 +282,16 @@ def clock_under_load(calls, dev, seconds: float = 1.5) -> dict:
             time.sleep(0.02)
 
     th = threading.Thread(target=sampler, daemon=True) if ddir else None
-    smi: dict = {}
-
-    # this device only: amd-smi lists every GPU of the host, ours by its PCI address
-    props = torch.cuda.get_device_properties(dev)
-    bdf = f"{props.pci_domain_id:04x}:{props.pci_bus_id:02x}:{props.pci_device_id:02x}.0"
-    out["amd_smi_gpu"] = bdf
-
-    def run_smi():
-        try:
-            r = subprocess.run(["amd-smi", "metric", "--gpu", bdf, "--clock"], capture_output=True, text=True,
-                               timeout=20)
-            smi["text"] = r.stdout
-            if r.returncode != 0:
-                smi["error"] = f"exit {r.returncode}: {r.stderr.strip()[:200]}"
-        except (OSError, subprocess.SubprocessError) as e:
-            smi["error"] = type(e).__name__
-
-    sm = threading.Thread(target=run_smi, daemon=True)
     if th:
         th.start()
     t0 = time.perf_counter()
-    started = False
-    # the launches go on until amd-smi has returned (it takes a second or more
-    # to start): read after the load, its clocks are the idle ones
-    while True:
-        el = time.perf_counter() - t0
-        if el >= seconds and not (started and sm.is_alive()):
-            break
-        if el >= seconds + 25.0:
-            break
+    while time.perf_counter() - t0 < seconds:
         for _, fn in calls:
             fn()
-        if not started and el > 0.3:
-            sm.start()
-            started = True
         torch.cuda.synchronize()
-    out["amd_smi_under_load"] = started and not sm.is_alive()
     stop.set()
     if th:
         th.join()
-    if started:
-        sm.join(timeout=25)
     if samples:
         s = sorted(samples)
         out["sysfs_pp_dpm_sclk_mhz"] = {"median": s[len(s) // 2], "min": s[0], "max": s[-1], "samples": len(s),
@@ -268,11 +299,6 @@ def clock_under_load(calls, dev, seconds: float = 1.5) -> dict:
     if power:
         p = sorted(power)
         out["board_power_w"] = {"median": round(p[len(p) // 2], 1), "max": round(p[-1], 1)}
-    gfx = [float(x) for x in re.findall(r"GFX_\d+:\s*\n\s*CLK:\s*([\d.]+)\s*MHz", smi.get("text", ""))]
-    if gfx:
-        out["amd_smi_gfx_clk_mhz"] = gfx
-    if "error" in smi:
-        out["amd_smi"] = smi["error"]
     return out
 
 
@@ -400,6 +426,9 @@ def main():
 
     if args.copy_calibration_mb > 0:
         copy_calibration(args.copy_calibration_mb)
+        return
+    if args.all_workloads:
+        all_workloads()
         return
 
     import torch
