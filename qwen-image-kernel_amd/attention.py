@@ -151,10 +151,14 @@ def block_causal_flash_attention(
         assert cache_v is not None and cache_v.shape[:3] == cache_k.shape[:3]
         _check_rows("cache_k", cache_k)
         _check_rows("cache_v", cache_v)
+    dev = query.device
+    for name, t in (("key", key), ("value", value)) + ((("cache_k", cache_k), ("cache_v", cache_v)) if P > 0 else ()):
+        if t.device != dev:
+            raise ValueError(f"{name} is on {t.device}, query on {dev}")
 
     out = torch.empty_like(query)
     if out.stride(-1) != 1:
-        out = torch.empty(query.shape, dtype=query.dtype, device=query.device)
+        out = torch.empty(query.shape, dtype=query.dtype, device=dev)
     if out.numel() == 0:
         # no query rows (or heads): the reference's grid is empty and it
         # returns the empty output without a launch
@@ -162,8 +166,11 @@ def block_causal_flash_attention(
 
     kv_bytes = None
     if key_valid is not None:
+        _check_aux("key_valid", key_valid, dev)
         kv_bytes = key_valid.to(torch.uint8).contiguous()
         assert kv_bytes.dim() == 2 and kv_bytes.shape[1] >= KV_TOTAL, "key_valid must be [B, KV_TOTAL]"
+        if kv_bytes.shape[0] not in (1, B):
+            raise ValueError(f"key_valid batch dim must be 1 or B={B}, got {kv_bytes.shape[0]}")
         if kv_bytes.shape[0] == 1 and B > 1:
             kv_bytes = kv_bytes.expand(B, -1)
 
@@ -171,6 +178,7 @@ def block_causal_flash_attention(
     scale = None
     if v_fp8:
         assert cache_v is not None and cache_v.dtype == torch.float8_e4m3fn
+        _check_aux("cache_v_scale", cache_v_scale, dev)
         scale = cache_v_scale
         if scale.dtype != torch.float32 or not scale.is_contiguous():
             scale = scale.float().contiguous()
@@ -182,59 +190,138 @@ def block_causal_flash_attention(
 
     L = None
     if not uniform:
+        _check_aux("prefix_lengths", prefix_lengths, dev)
         L = prefix_lengths
         if L.dtype != torch.int32 or not L.is_contiguous():
             L = L.to(torch.int32).contiguous()
         assert L.numel() >= SQ, "prefix_lengths must be [SQ]"
 
+    if debug_tiles is not None:
+        _check_aux("debug_tiles", debug_tiles, dev)
+        need = B * H * -(-SQ // block_shape()[0])
+        if debug_tiles.dtype != torch.int32 or not debug_tiles.is_contiguous() or debug_tiles.numel() < need:
+            raise ValueError(f"debug_tiles must be a contiguous int32 tensor of at least {need} elements")
+
     # with P == 0 the slab (and its fp8 scale) is never read (HAS_CACHE = P > 0, :250)
-    args = make_args(query, key, value, L, kv_bytes, out, cache_k if P > 0 else None,
-                     cache_v if P > 0 else None, scale if P > 0 else None, uniform, debug_tiles)
-    dev = query.device
+    if P == 0:
+        cache_k = cache_v = scale = None
+    args, ws_bytes = _cached_args(query, key, value, L, kv_bytes, out, cache_k, cache_v, scale, uniform,
+                                  debug_tiles, split_tail)
     if dev.index is not None and dev.index != torch.cuda.current_device():
         with torch.cuda.device(dev):
-            _launch(args, dev, split_tail)
+            _launch(args, dev, split_tail, ws_bytes)
     else:
-        _launch(args, dev, split_tail)
+        _launch(args, dev, split_tail, ws_bytes)
     return out
 
 
-_WORKSPACES: dict = {}  # (device index, stream handle) -> zeroed uint8 tensor
+def _check_aux(name: str, t: torch.Tensor, dev: torch.device) -> None:
+    """The side inputs go to the kernel as raw device addresses: they must live on the query's device."""
+    if not isinstance(t, torch.Tensor):
+        raise ValueError(f"{name} must be a tensor on {dev}")
+    if t.device != dev:
+        raise ValueError(f"{name} is on {t.device}; it must be on the query's device {dev}")
+
+
+# Argument structs by call geometry: everything of qik_attn_args except the
+# data pointers, plus the workspace size the launch needs.  Building the
+# struct and asking the library for the size cost more host time than a
+# small launch takes on the device, so both are done once per geometry.
+_ARGS_CACHE: dict = {}
+_ARGS_CACHE_MAX = 256
+
+
+def _geometry(query, key, value, L, kv_bytes, out, cache_k, cache_v, scale, uniform, debug, split_tail):
+    return (
+        query.device, query.dtype, tuple(query.shape), query.stride(), key.shape[1], key.stride(), value.stride(),
+        out.stride(),
+        None if cache_k is None else (cache_k.shape[1], cache_k.stride(), cache_v.stride(), cache_v.dtype),
+        L is None, uniform, None if kv_bytes is None else kv_bytes.stride(0), scale is None, debug is None,
+        split_tail,
+    )
+
+
+def _cached_args(query, key, value, L, kv_bytes, out, cache_k, cache_v, scale, uniform, debug, split_tail):
+    gkey = _geometry(query, key, value, L, kv_bytes, out, cache_k, cache_v, scale, uniform, debug, split_tail)
+    hit = _ARGS_CACHE.get(gkey)
+    if hit is None:
+        a = make_args(query, key, value, L, kv_bytes, out, cache_k, cache_v, scale, uniform, debug)
+        ws_bytes = 0
+        if split_tail:
+            lib = _lib.load()
+            nbytes = ctypes.c_int64(0)
+            with torch.cuda.device(query.device):
+                _lib.check(lib.qik_attn_workspace_size(ctypes.byref(a), ctypes.byref(nbytes)),
+                           "qik_attn_workspace_size")
+            ws_bytes = nbytes.value
+        if len(_ARGS_CACHE) >= _ARGS_CACHE_MAX:
+            _ARGS_CACHE.clear()
+        _ARGS_CACHE[gkey] = (_lib.QikAttnArgs.from_buffer_copy(a), ws_bytes)
+        return a, ws_bytes
+    a = _lib.QikAttnArgs.from_buffer_copy(hit[0])
+    a.q = query.data_ptr()
+    a.k_new = key.data_ptr()
+    a.v_new = value.data_ptr()
+    a.out = out.data_ptr()
+    a.prefix_lengths = None if L is None else L.data_ptr()
+    a.key_valid = None if kv_bytes is None else kv_bytes.data_ptr()
+    a.debug_tiles = None if debug is None else debug.data_ptr()
+    if cache_k is not None:
+        a.k_cache = cache_k.data_ptr()
+        a.v_cache = cache_v.data_ptr()
+        a.v_scale = None if scale is None else scale.data_ptr()
+    return a, hit[1]
+
+
+# (device index, stream handle) -> workspace of one stream, control words zero.
+# Bounded: a program that cycles through many streams drops the oldest.
+_WORKSPACES: dict = {}
+_WORKSPACES_MAX = 16
 
 
 def _workspace(dev: torch.device, stream: int, nbytes: int) -> torch.Tensor:
-    """A workspace for qik_attn_fwd_ws, zeroed when created.
+    """A workspace for qik_attn_fwd_ws whose control words are zero.
 
-    Every launch leaves the control words zero again, so one workspace per
-    (device, stream) is kept and reused; launches on one stream never overlap.
-    Under graph capture a fresh zeroed workspace is taken from the graph's
-    pool instead (its zeroing is captured too), so a replay never shares the
-    cached one with eager launches.
+    Every launch leaves the control words (the first ``WS_CTL_BYTES``) zero
+    again, so one workspace per (device, stream) is kept and reused; launches
+    on one stream never overlap.  Under graph capture a fresh workspace is
+    taken from the graph's pool instead, and only its control words are
+    cleared (by a captured fill kernel), so a replay never shares the cached
+    one with eager launches; the partial-state slots behind them are always
+    written before they are read.
     """
     if torch.cuda.is_current_stream_capturing():
-        return torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        ws[: min(nbytes, _lib.WS_CTL_BYTES)].zero_()
+        return ws
     key = (dev.index, stream)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+        if ws is None and len(_WORKSPACES) >= _WORKSPACES_MAX:
+            _WORKSPACES.pop(next(iter(_WORKSPACES)))
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        ws[: min(nbytes, _lib.WS_CTL_BYTES)].zero_()
         _WORKSPACES[key] = ws
     return ws
 
 
-def _launch(args: _lib.QikAttnArgs, dev: torch.device, split_tail: bool) -> None:
+def _current_stream(dev: torch.device) -> int:
+    """Raw handle of the current stream of ``dev`` (the current device)."""
+    return torch._C._cuda_getCurrentRawStream(dev.index if dev.index is not None else torch.cuda.current_device())
+
+
+def _launch(args: _lib.QikAttnArgs, dev: torch.device, split_tail: bool, ws_bytes: int) -> None:
     """Enqueue the kernel on the current stream of ``dev`` (the current device)."""
     lib = _lib.load()
-    handle = torch.cuda.current_stream(dev).cuda_stream
+    handle = _current_stream(dev)
     stream = ctypes.c_void_p(handle)
     if not split_tail:
         _lib.check(lib.qik_attn_fwd(ctypes.byref(args), stream), "qik_attn_fwd")
         return
-    nbytes = ctypes.c_int64(0)
-    _lib.check(lib.qik_attn_workspace_size(ctypes.byref(args), ctypes.byref(nbytes)), "qik_attn_workspace_size")
-    ws = None if nbytes.value == 0 else _workspace(dev if dev.index is not None else
-                                                   torch.device("cuda", torch.cuda.current_device()),
-                                                   handle, nbytes.value)
-    st = lib.qik_attn_fwd_ws(ctypes.byref(args), None if ws is None else ws.data_ptr(), nbytes.value, stream)
+    ws = None if ws_bytes == 0 else _workspace(dev if dev.index is not None else
+                                               torch.device("cuda", torch.cuda.current_device()),
+                                               handle, ws_bytes)
+    st = lib.qik_attn_fwd_ws(ctypes.byref(args), None if ws is None else ws.data_ptr(), ws_bytes, stream)
     _lib.check(st, "qik_attn_fwd_ws")
 
 

@@ -6,10 +6,17 @@
 // an optional key_valid byte mask gates keys, and the slab V may be fp8e4m3fn
 // with one fp32 scale per (b, h).  Rounding points kept from the reference:
 //   S      = fp32 MFMA accumulation of bf16 Q.K, scaled by qk_scale = sm_scale*log2(e)
-//   p      = exp2(S - m)  in fp32;  l = l*alpha + sum(p) uses the fp32 p
+//   p      = exp2(S*qk_scale - m) in fp32; l = l*alpha + sum(p) uses the fp32 p
 //   P      = bf16(p) (RNE) feeds the PV MFMA
 //   V_slab = bf16(fp32(v_fp8) * v_scale[b,h])   (fp32 multiply, RNE to bf16)
-//   out    = l > 0 ? acc / l : 0, stored RNE in the output dtype
+//   out    = l > 0 ? acc * (1/l) : 0, stored RNE in the output dtype
+// Deviations from the reference's arithmetic, all at fp32 rounding level:
+//   * the exp2 reference point m is lazy: it moves only when a row's max grows
+//     by more than TAU = 8 (log2 units), so p <= 2^8 and the O rescale is
+//     skipped on almost every tile (the reference moves m to every new max);
+//   * the epilogue multiplies by one reciprocal of l per row instead of
+//     dividing every element;
+//   * exp2 is the hardware v_exp_f32.
 //
 // Work decomposition (one workgroup = BM=128 query rows of one (b, h)):
 //   * 4 waves x 32 rows.  Each wave computes S^T = K.Q^T with the MFMA

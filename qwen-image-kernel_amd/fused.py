@@ -65,14 +65,42 @@ def fused_rms_norm_rope(
         x = x.contiguous()
     if tuple(freqs_cis.shape) != (S, D // 2):
         raise ValueError(f"freqs_cis must be [S, D/2] = {(S, D // 2)}, got {tuple(freqs_cis.shape)}")
-    w = weight.to(device=x.device, dtype=torch.float32).contiguous()
+    w = weight
+    if w.dtype != torch.float32 or w.device != x.device or not w.is_contiguous():
+        w = weight.to(device=x.device, dtype=torch.float32).contiguous()
     cos, sin = _cos_sin(freqs_cis, x.device)
     out = torch.empty((B, S, H, D), dtype=x.dtype, device=x.device)
-    a = rms_rope_args(x, w, cos, sin, out, eps)
-    with torch.cuda.device(x.device):
-        stream = torch.cuda.current_stream(x.device).cuda_stream
-        _lib.check(_lib.load().qik_rms_rope(ctypes.byref(a), stream), "qik_rms_rope")
+    a = _cached_args(x, w, cos, sin, out, eps)
+    lib = _lib.load()
+    idx = x.device.index
+    if idx != torch.cuda.current_device():
+        with torch.cuda.device(x.device):
+            _lib.check(lib.qik_rms_rope(ctypes.byref(a), torch._C._cuda_getCurrentRawStream(idx)), "qik_rms_rope")
+    else:
+        _lib.check(lib.qik_rms_rope(ctypes.byref(a), torch._C._cuda_getCurrentRawStream(idx)), "qik_rms_rope")
     return out
+
+
+# Argument structs by geometry (shapes, strides, dtype, eps); only the data
+# pointers change from call to call.  Filling the struct field by field costs
+# more host time than the launch takes on the device.
+_ARGS_CACHE: dict = {}
+
+
+def _cached_args(x, w, cos, sin, out, eps) -> _lib.QikRmsRopeArgs:
+    gkey = (x.device, x.dtype, tuple(x.shape), x.stride(), out.stride(), float(eps))
+    hit = _ARGS_CACHE.get(gkey)
+    if hit is None:
+        if len(_ARGS_CACHE) >= 64:
+            _ARGS_CACHE.clear()
+        hit = _ARGS_CACHE[gkey] = rms_rope_args(x, w, cos, sin, out, eps)
+    a = _lib.QikRmsRopeArgs.from_buffer_copy(hit)
+    a.x = x.data_ptr()
+    a.out = out.data_ptr()
+    a.weight = w.data_ptr()
+    a.cos = cos.data_ptr()
+    a.sin = sin.data_ptr()
+    return a
 
 
 def rms_rope_args(x, weight, cos, sin, out, eps) -> _lib.QikRmsRopeArgs:

@@ -23,6 +23,7 @@ import torch
 
 from .attention import block_causal_flash_attention, build_prefix_lengths
 from .fused import fused_rms_norm_rope
+from .kv_cache import _LayerView
 
 __all__ = ["QwenImage21KernelProcessor", "_build_prefix_lengths"]
 
@@ -74,8 +75,14 @@ class QwenImage21KernelProcessor:
         key = fused_rms_norm_rope(key, attn.norm_k.weight, rotary_emb, attn.norm_k.eps)
 
         if kv_cache_mode == "extract" and layer_cache is not None and cache_write_slice is not None:
-            # the slab store reads the slices in place (the reference clones them)
-            layer_cache.store(key[:, cache_write_slice], value[:, cache_write_slice])
+            k_pre, v_pre = key[:, cache_write_slice], value[:, cache_write_slice]
+            if not isinstance(layer_cache, _LayerView):
+                # a cache that keeps the tensors it is given (the stock get()-only
+                # cache) gets copies, as processors.py:83-84 hands it, so that it
+                # does not pin the whole K/V (or fused QKV output) of the layer
+                k_pre, v_pre = k_pre.clone(), v_pre.clone()
+            # ContiguousKVCache copies into its slab: the slices are read in place
+            layer_cache.store(k_pre, v_pre)
 
         if segments is not None:
             # prefill over the full joint sequence (processors.py:86-94)

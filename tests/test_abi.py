@@ -285,3 +285,17 @@ def test_slab_store_workspace_checks_and_size():
     assert lib.qik_slab_store_ws(ctypes.byref(_store_args()), base + 2, 512, None) == WS
     # no rows: nothing to do, no workspace looked at
     assert lib.qik_slab_store_ws(ctypes.byref(_store_args(P=0, k=None)), None, 0, None) == 0
+
+
+def test_side_input_device_check_is_host_side():
+    """A side input that is not on the query's device raises ValueError before any launch."""
+    import torch
+
+    cpu = torch.zeros(4, dtype=torch.int32)
+    with pytest.raises(ValueError, match="prefix_lengths"):
+        attention._check_aux("prefix_lengths", cpu, torch.device("cuda", 0))
+    with pytest.raises(ValueError, match="key_valid"):
+        attention._check_aux("key_valid", cpu.bool(), torch.device("cuda", 0))
+    with pytest.raises(ValueError, match="cache_v_scale"):
+        attention._check_aux("cache_v_scale", None, torch.device("cuda", 0))
+    attention._check_aux("prefix_lengths", cpu, torch.device("cpu"))

@@ -321,6 +321,50 @@ def test_misaligned_input_is_rejected():
         qik.block_causal_flash_attention(q, q, q, L, None)
 
 
+def test_side_inputs_on_the_host_or_misshaped_are_rejected():
+    """prefix_lengths, key_valid, cache_v_scale and debug_tiles reach the kernel as raw
+    device addresses: host tensors, a key_valid batch that is neither 1 nor B, and an
+    undersized or non-int32 debug_tiles raise before any launch."""
+    g = torch.Generator().manual_seed(961)
+    q, k, v = (_rand((2, 128, 2, 128), g).to(DEV) for _ in range(3))
+    L = torch.arange(128, dtype=torch.int32)
+    with pytest.raises(ValueError, match="prefix_lengths"):
+        qik.block_causal_flash_attention(q, k, v, L, None)
+    Ld = L.to(DEV)
+    with pytest.raises(ValueError, match="key_valid"):
+        qik.block_causal_flash_attention(q, k, v, Ld, torch.ones(2, 128, dtype=torch.bool))
+    with pytest.raises(ValueError, match="batch dim"):
+        qik.block_causal_flash_attention(q, k, v, Ld, torch.ones(3, 128, dtype=torch.bool, device=DEV))
+    with pytest.raises(ValueError, match="debug_tiles"):
+        qik.block_causal_flash_attention(q, k, v, Ld, None, debug_tiles=torch.zeros(3, dtype=torch.int32, device=DEV))
+    with pytest.raises(ValueError, match="debug_tiles"):
+        qik.block_causal_flash_attention(q, k, v, Ld, None, debug_tiles=torch.zeros(4, dtype=torch.int64, device=DEV))
+    kc = _rand((2, 64, 2, 128), g).to(DEV)
+    vc = kc.to(torch.float8_e4m3fn)
+    with pytest.raises(ValueError, match="cache_v_scale"):
+        qik.block_causal_flash_attention(q, k, v, Ld, None, cache_k=kc, cache_v=vc,
+                                         cache_v_scale=torch.ones(2, 2))
+    # the same call with every side input on the device runs
+    qik.block_causal_flash_attention(q, k, v, Ld, torch.ones(1, 192, dtype=torch.bool, device=DEV), cache_k=kc,
+                                     cache_v=vc, cache_v_scale=torch.ones(2, 2, device=DEV),
+                                     debug_tiles=torch.zeros(4, dtype=torch.int32, device=DEV))
+    torch.cuda.synchronize()
+
+
+def test_cached_arguments_follow_new_pointers():
+    """The wrapper keeps the argument struct per geometry: a second call of the same
+    geometry with other tensors must read those tensors."""
+    g = torch.Generator().manual_seed(962)
+    L = torch.arange(300, dtype=torch.int32, device=DEV)
+    outs = []
+    for _ in range(2):
+        q, k, v = (_rand((1, 300, 3, 128), g).to(DEV) for _ in range(3))
+        out = qik.block_causal_flash_attention(q, k, v, L, None)
+        _check(out, oa.attention_fp32(q.cpu(), k.cpu(), v.cpu(), L.cpu().numpy()), what="cached args")
+        outs.append(out)
+    assert not torch.equal(outs[0], outs[1])
+
+
 # ---------------------------------------------------------------------------
 # causal lengths and the visited-tile schedule: bit-exact
 
