@@ -49,7 +49,8 @@ enum qik_status {
   QIK_ERR_LAUNCH = -9,        /* the HIP launch failed                               */
   QIK_ERR_SEGMENTS = -10,     /* bad segment list for the causal-length builder      */
   QIK_ERR_DEVICE = -11,       /* no usable HIP device / device query failed          */
-  QIK_ERR_WORKSPACE = -12     /* workspace NULL, misaligned or too small (qik_attn_fwd_ws) */
+  QIK_ERR_WORKSPACE = -12,    /* workspace NULL, misaligned or too small (qik_attn_fwd_ws) */
+  QIK_ERR_SCRATCH = -13       /* the call needs more than QIK_ATTN_SCRATCH_BYTES (qik_attn_fwd_noalloc) */
 };
 
 /* Arguments of one attention call.  Layouts are [B, S, H, D] with the D
@@ -138,6 +139,24 @@ int qik_attn_workspace_size(const qik_attn_args* args, int64_t* bytes);
  * on another.  Replaces the same Triton launch as qik_attn_fwd
  * (triton_attention.py:234-259); the reference has no workspace. */
 int qik_attn_fwd_ws(const qik_attn_args* args, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Bytes of the device array behind qik_attn_fwd_noalloc, held on every device
+ * the library runs on until the process ends. */
+#define QIK_ATTN_SCRATCH_BYTES (72 * 1024 * 1024)
+
+/* qik_attn_fwd_ws without a caller workspace, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
+ * workspace is a static device array of QIK_ATTN_SCRATCH_BYTES in this
+ * library, one per device; the call clears its control words with a fill
+ * kernel on `stream`, then runs the same kernel and work plan as
+ * qik_attn_fwd_ws (bit-identical results).  It calls no hipMalloc/hipFree.
+ * A call that needs more than QIK_ATTN_SCRATCH_BYTES (qik_attn_workspace_size)
+ * returns QIK_ERR_SCRATCH; every shape with D <= 128 fits on MI355X.  All
+ * calls on one device share the array: calls that may overlap in time
+ * (different streams, or different host threads) race and must not be
+ * issued. */
+int qik_attn_fwd_noalloc(const qik_attn_args* args, void* stream);
 
 /* Host mirror of the workgroup -> work assignment (no device): for n_items
  * row blocks (n_row_blocks per (b, h)) and `slots_per_xcd` workgroups

@@ -48,7 +48,11 @@ STATUS_NAMES = {
     -10: "QIK_ERR_SEGMENTS",
     -11: "QIK_ERR_DEVICE",
     -12: "QIK_ERR_WORKSPACE",
+    -13: "QIK_ERR_SCRATCH",
 }
+
+# bytes of the static device array behind qik_attn_fwd_noalloc
+ATTN_SCRATCH_BYTES = 72 * 1024 * 1024
 
 _i64x3 = ctypes.c_int64 * 3
 
@@ -148,6 +152,7 @@ EXPORTS = (
         ctypes.c_int,
         (ctypes.POINTER(QikAttnArgs), ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p),
     ),
+    ("qik_attn_fwd_noalloc", ctypes.c_int, (ctypes.POINTER(QikAttnArgs), ctypes.c_void_p)),
     (
         "qik_attn_work_map",
         ctypes.c_int,

@@ -765,6 +765,19 @@ __global__ void build_lengths_kernel(const SegList segs, int init, int apply_pre
 }
 
 // ---------------------------------------------------------------------------
+// The workspace of qik_attn_fwd_noalloc: one array per device, never
+// allocated by the library.  Host code uses its device address from
+// hipGetSymbolAddress (scratch_ptr below), never the name.
+static __device__ __align__(256) unsigned char scratch[QIK_ATTN_SCRATCH_BYTES];
+
+// Zero `n16` 16-byte words (the scratch's control words) with vector stores;
+// a fill kernel rather than hipMemsetAsync, so that a captured graph replays it.
+__global__ void zero16_kernel(u32x4* p, int n16) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n16) p[i] = u32x4{0u, 0u, 0u, 0u};
+}
+
+// ---------------------------------------------------------------------------
 // host side
 
 typedef void (*kernel_fn)(Params);
@@ -883,6 +896,21 @@ int plan_launch(const qik_attn_args* a, bool split, Launch* L) {
   return QIK_OK;
 }
 
+// Device address of `scratch` on the current device, resolved once per device.
+std::atomic<void*> g_scratch[MAX_DEVICES];
+
+int scratch_ptr(void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return QIK_ERR_DEVICE;
+  void* p = g_scratch[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) return QIK_ERR_DEVICE;
+    g_scratch[dev].store(p, std::memory_order_release);
+  }
+  *out = p;
+  return QIK_OK;
+}
+
 int launch(const qik_attn_args* a, bool split, void* ws, int64_t ws_bytes, void* stream) {
   const int st = qik_attn_validate(a);
   if (st != QIK_OK) return st;
@@ -956,6 +984,7 @@ const char* qik_strerror(int status) {
     case QIK_ERR_SEGMENTS: return "segments need 0 <= start <= end, and 0 <= prefix_end <= seq_len";
     case QIK_ERR_DEVICE: return "HIP device query failed";
     case QIK_ERR_WORKSPACE: return "workspace NULL, not 256-byte aligned, or smaller than qik_attn_workspace_size";
+    case QIK_ERR_SCRATCH: return "the call needs more workspace than QIK_ATTN_SCRATCH_BYTES";
     default: return "unknown qik status";
   }
 }
@@ -1039,6 +1068,28 @@ int qik_attn_workspace_size(const qik_attn_args* a, int64_t* bytes) {
 
 int qik_attn_fwd_ws(const qik_attn_args* a, void* workspace, int64_t workspace_bytes, void* stream) {
   return qik::launch(a, true, workspace, workspace_bytes, stream);
+}
+
+int qik_attn_fwd_noalloc(const qik_attn_args* a, void* stream) {
+  const int st = qik_attn_validate(a);
+  if (st != QIK_OK) return st;
+  qik::Launch L;
+  const int pst = qik::plan_launch(a, true, &L);
+  if (pst != QIK_OK) return pst;
+  if (L.grid == 0) return QIK_OK;
+  if (L.ws_bytes > (int64_t)QIK_ATTN_SCRATCH_BYTES) return QIK_ERR_SCRATCH;
+  void* ws = nullptr;
+  if (L.ws_bytes > 0) {
+    const int sst = qik::scratch_ptr(&ws);
+    if (sst != QIK_OK) return sst;
+    // the control words must be zero when the attention launch starts
+    const int n16 = (int)(L.ctl_bytes / 16);
+    void* kargs[] = {&ws, (void*)&n16};
+    if (hipLaunchKernel(reinterpret_cast<const void*>(qik::zero16_kernel), dim3((unsigned)((n16 + 255) / 256)),
+                        dim3(256), kargs, 0, static_cast<hipStream_t>(stream)) != hipSuccess)
+      return QIK_ERR_LAUNCH;
+  }
+  return qik::launch(a, true, ws, (int64_t)QIK_ATTN_SCRATCH_BYTES, stream);
 }
 
 int qik_attn_work_map(int64_t n_items, int32_t n_row_blocks, int32_t slots_per_xcd, int32_t split,

@@ -299,3 +299,9 @@ def test_side_input_device_check_is_host_side():
     with pytest.raises(ValueError, match="cache_v_scale"):
         attention._check_aux("cache_v_scale", None, torch.device("cuda", 0))
     attention._check_aux("prefix_lengths", cpu, torch.device("cpu"))
+
+
+def test_scratch_constant_matches_the_binding():
+    text = open(HEADER).read()
+    m = re.search(r"#define QIK_ATTN_SCRATCH_BYTES \((\d+) \* 1024 \* 1024\)", text)
+    assert int(m.group(1)) * 1024 * 1024 == _lib.ATTN_SCRATCH_BYTES
