@@ -1,0 +1,108 @@
+/*
+ * qik_fp8.h -- C ABI of the W8A8 fp8 linear of a Qwen-Image 2.1 DiT layer
+ * (replaces the device work of `FP8Linear.forward`, qwen_image_kernel/fp8.py:78-90):
+ *
+ *   qik_fp8_quantize  per-tensor fp8e4m3fn quantisation of an activation
+ *                     (`quantize_tensorwise`, fp8.py:24-53) or of a weight
+ *                     (`quantize_weight_tensorwise`, fp8.py:56-60)
+ *   qik_fp8_gemm      out = (A_fp8 . W_fp8^T) * (scale_a * scale_b) + bias
+ *                     (the `torch._scaled_mm` call, fp8.py:87-88)
+ *   qik_fp8_dequant   bf16(fp32(w_fp8) * scale), the weight of the bf16 path
+ *                     that layers with fewer than 256 inputs take (fp8.py:79-84)
+ *
+ * Same conventions as qik_attn.h: plain C, no allocation, device pointers of
+ * the current HIP device, `stream` a hipStream_t as void*, asynchronous and
+ * stream-ordered launches, return QIK_OK or a negative qik_status.  fp8 data
+ * is OCP e4m3fn (bias 7, max 448, 0x7f / 0xff NaN), one byte per element.
+ */
+#ifndef QIK_FP8_H
+#define QIK_FP8_H
+
+#include <stdint.h>
+
+#include "qik_attn.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element type of a quantiser input (in addition to QIK_DTYPE_BF16 / _FP16). */
+#define QIK_DTYPE_FP32 2
+
+/* How qik_fp8_quantize forms the codes once the scale is known. */
+enum qik_fp8_mode {
+  QIK_FP8_ACTIVATION = 0,  /* code = e4m3_rne(x * (1 / scale))            (fp8.py:28-40) */
+  QIK_FP8_WEIGHT = 1       /* code = e4m3_rne(clamp(x / scale, +-448))    (fp8.py:58-59) */
+};
+
+/* Per-tensor quantisation of n contiguous elements:
+ *   amax  = max |x|                                      (fp32; NaN if any x is NaN)
+ *   scale = max(amax * fp32(1/448), fp32(1e-12))          (NaN stays NaN)
+ *   out   = codes by `mode`; *scale_out = scale
+ * The scale is what torch computes on a HIP device for
+ * (x.abs().amax().float() / 448.0).clamp_min(1e-12): a tensor divided by a
+ * Python scalar is multiplied by the scalar's fp32 reciprocal there.  The
+ * activation form takes the reciprocal of the scale once (IEEE fp32 division)
+ * and multiplies, as the reference's cast kernel does; the weight form divides
+ * every element (IEEE) and clamps, as the reference's weight quantiser does.
+ * Both round to nearest even.  Finite inputs give codes bit-identical to those
+ * torch ops on the device; a non-finite input makes the scale non-finite and
+ * the codes NaN or zero, as in the reference ("non-finite inputs poison the
+ * output", fp8.py:33-34).
+ * x: 16-byte aligned; out: aligned to the bytes one 16-byte vector of x
+ * yields (8 for bf16/fp16, 4 for fp32). */
+typedef struct qik_fp8_quant_args {
+  int32_t abi_version;        /* QIK_ABI_VERSION                                     */
+  int32_t dtype;              /* QIK_DTYPE_BF16, QIK_DTYPE_FP16 or QIK_DTYPE_FP32      */
+  int32_t mode;               /* enum qik_fp8_mode                                   */
+  int32_t reserved0;          /* must be 0                                           */
+  const void* x;              /* [n] input                                           */
+  void* out;                  /* [n] fp8e4m3fn codes                                 */
+  float* scale;               /* [1] fp32, written                                   */
+  int64_t n;                  /* elements, 1 <= n < 2^40                             */
+} qik_fp8_quant_args;
+
+/* Two launches: per-block partial maxima into the caller's workspace (at least
+ * qik_fp8_quant_workspace_size bytes, 4-byte aligned, contents irrelevant: every
+ * launch writes what it reads), then the codes.  QIK_ERR_WORKSPACE for a
+ * missing, misaligned or short workspace. */
+int qik_fp8_quant_workspace_size(const qik_fp8_quant_args* args, int64_t* bytes);
+int qik_fp8_quantize(const qik_fp8_quant_args* args, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* out[m, n] = round(fp32(sum_k A[m, k] * W[n, k]) * (scale_a * scale_b) + bias[n])
+ * with fp32 accumulation of the exact fp8 products, the two scales multiplied
+ * once in fp32, the bias (if any) added in fp32 and one round to nearest even
+ * into the output dtype: torch._scaled_mm(A, W.t(), scale_a, scale_b, bias,
+ * out_dtype) with tensorwise scales.  Both operands are K-contiguous (row
+ * strides lda / ldb in bytes, multiples of 16 and >= K); out is N-contiguous
+ * with row stride ldc elements.  K and N multiples of 16 (as the _scaled_mm
+ * contract requires), M >= 1.  Pointers 16-byte aligned (bias: 8). */
+typedef struct qik_fp8_gemm_args {
+  int32_t abi_version;        /* QIK_ABI_VERSION                                     */
+  int32_t out_dtype;          /* QIK_DTYPE_BF16 or QIK_DTYPE_FP16 (bias has it too)   */
+  int32_t reserved0;          /* must be 0                                           */
+  int32_t reserved1;          /* must be 0                                           */
+  const void* a;              /* [M, K] fp8e4m3fn activations                        */
+  const void* w;              /* [N, K] fp8e4m3fn weight                             */
+  const float* scale_a;       /* [1] fp32 device scalar                              */
+  const float* scale_w;       /* [1] fp32 device scalar                              */
+  const void* bias;           /* [N] in out_dtype, or NULL                           */
+  void* out;                  /* [M, N] in out_dtype                                 */
+  int64_t M, N, K;
+  int64_t lda, ldw;           /* row strides of a and w, bytes                       */
+  int64_t ldc;                /* row stride of out, elements                         */
+} qik_fp8_gemm_args;
+
+int qik_fp8_gemm_validate(const qik_fp8_gemm_args* args);
+int qik_fp8_gemm(const qik_fp8_gemm_args* args, void* stream);
+
+/* out[i] = round(fp32(code[i]) * scale[0]) into out_dtype (bf16 or fp16), for
+ * i < n: the dequantised weight of the bf16 path (fp8.py:81: fp8 -> bf16 ->
+ * fp32 is exact, one fp32 multiply, one round).  w 8-byte aligned, out 16. */
+int qik_fp8_dequant(const void* w, const float* scale, void* out, int64_t n, int32_t out_dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QIK_FP8_H */

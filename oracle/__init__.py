@@ -15,8 +15,10 @@ qwen-image-kernel reference repository):
 * ``schedule``  -- KV-tile schedule per row block: the reference rule
                    (triton_attention.py:79-83, 95, 115-121) and the exact rule.
 * ``fp8``       -- OCP e4m3fn decode/encode from the format definition, the per-(b,h)
-                   slab quantisation (kv_cache.py:36-42) and the in-kernel dequant
-                   rounding point (triton_attention.py:154-159).
+                   slab quantisation (kv_cache.py:36-42), the in-kernel dequant
+                   rounding point (triton_attention.py:154-159), and the W8A8 linear:
+                   per-tensor activation / weight quantisation (fp8.py:24-60) and the
+                   tensorwise-scaled GEMM (fp8.py:87-88) in fp64.
 * ``attention`` -- fp32 explicit-mask attention (triton_attention.py:266-293) extended
                    with fp8 slab V, plus an fp64 brute force for tiny inputs, and the
                    explicit-mask SDPA CPU baseline.

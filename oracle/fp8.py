@@ -88,3 +88,53 @@ def dequant_bf16(codes: np.ndarray, scale) -> np.ndarray:
     """
     vals = _TABLE[np.asarray(codes, dtype=np.uint8)]
     return bf16_round(vals * np.asarray(scale, dtype=np.float32))
+
+
+def tensor_scale(x: np.ndarray) -> np.float32:
+    """Per-tensor scale of fp8.py:24-26 / :58 as torch forms it on a GPU:
+    max(amax|x| * fp32(1/448), 1e-12) (a tensor divided by the host scalar 448
+    is multiplied by its fp32 reciprocal there; clamp_min keeps NaN)."""
+    a = np.abs(np.asarray(x, dtype=np.float32)).max()
+    if np.isnan(a):
+        return np.float32(np.nan)
+    inv = np.float32(1.0) / np.float32(E4M3_MAX)
+    return np.float32(max(np.float32(a * inv), np.float32(1e-12)))
+
+
+def quantize_tensorwise(x: np.ndarray) -> tuple[np.ndarray, np.float32]:
+    """Activation quantisation of fp8.py:43-53: scale as tensor_scale, then
+    code = e4m3(x * fp32(1 / scale)) (the reciprocal is one correctly rounded
+    fp32 division, fp8.py:37), no clamp (|x * (1/scale)| < 464 for finite x)."""
+    x = np.asarray(x, dtype=np.float32)
+    s = tensor_scale(x)
+    inv = np.float32(1.0) / s
+    return e4m3fn_encode((x * inv).astype(np.float32)), s
+
+
+def quantize_weight_tensorwise(w: np.ndarray) -> tuple[np.ndarray, np.float32]:
+    """Weight quantisation of fp8.py:56-60: code = e4m3(clamp(w / scale, +-448))
+    with a correctly rounded fp32 division per element."""
+    w = np.asarray(w, dtype=np.float32)
+    s = tensor_scale(w)
+    q = np.clip((w / s).astype(np.float32), -E4M3_MAX, E4M3_MAX).astype(np.float32)
+    return e4m3fn_encode(q), s
+
+
+def decode(codes: np.ndarray) -> np.ndarray:
+    """fp32 values of e4m3fn codes (exact)."""
+    return _TABLE[np.asarray(codes, dtype=np.uint8)]
+
+
+def scaled_mm(a_codes: np.ndarray, w_codes: np.ndarray, scale_a, scale_w, bias=None) -> np.ndarray:
+    """fp64 value of what torch._scaled_mm(A, W.t(), scale_a, scale_b, bias)
+    computes with tensorwise scales (fp8.py:87-88), before the final rounding:
+    (sum_k A[m,k] W[n,k]) * fp32(scale_a * scale_w) + bias[n].  The fp8
+    products are exact in fp64 and their fp64 sum is far closer to the exact
+    sum than any fp32 accumulation, so this is the target an fp32-accumulating
+    GEMM approaches.  Returns float64 [M, N]."""
+    acc = decode(a_codes).astype(np.float64) @ decode(w_codes).astype(np.float64).T
+    ab = np.float64(np.float32(np.float32(scale_a) * np.float32(scale_w)))
+    out = acc * ab
+    if bias is not None:
+        out = out + np.asarray(bias, dtype=np.float64)[None, :]
+    return out

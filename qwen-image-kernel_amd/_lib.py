@@ -25,6 +25,10 @@ ABI_VERSION = 1
 
 DTYPE_BF16 = 0
 DTYPE_FP16 = 1
+DTYPE_FP32 = 2  # quantiser input only (include/qik_fp8.h)
+
+FP8_ACTIVATION = 0
+FP8_WEIGHT = 1
 
 # leading bytes of a qik_attn_fwd_ws workspace that hold its control words
 WS_CTL_BYTES = 32768
@@ -139,6 +143,44 @@ class QikSlabStoreArgs(ctypes.Structure):
     ]
 
 
+class QikFp8QuantArgs(ctypes.Structure):
+    """Mirror of ``struct qik_fp8_quant_args`` (include/qik_fp8.h)."""
+
+    _fields_ = [
+        ("abi_version", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("mode", ctypes.c_int32),
+        ("reserved0", ctypes.c_int32),
+        ("x", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("scale", ctypes.c_void_p),
+        ("n", ctypes.c_int64),
+    ]
+
+
+class QikFp8GemmArgs(ctypes.Structure):
+    """Mirror of ``struct qik_fp8_gemm_args`` (include/qik_fp8.h)."""
+
+    _fields_ = [
+        ("abi_version", ctypes.c_int32),
+        ("out_dtype", ctypes.c_int32),
+        ("reserved0", ctypes.c_int32),
+        ("reserved1", ctypes.c_int32),
+        ("a", ctypes.c_void_p),
+        ("w", ctypes.c_void_p),
+        ("scale_a", ctypes.c_void_p),
+        ("scale_w", ctypes.c_void_p),
+        ("bias", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("M", ctypes.c_int64),
+        ("N", ctypes.c_int64),
+        ("K", ctypes.c_int64),
+        ("lda", ctypes.c_int64),
+        ("ldw", ctypes.c_int64),
+        ("ldc", ctypes.c_int64),
+    ]
+
+
 # (name, restype, argtypes) of every exported entry point
 EXPORTS = (
     ("qik_abi_version", ctypes.c_int, ()),
@@ -175,6 +217,14 @@ EXPORTS = (
     ("qik_slab_store_workspace_size", ctypes.c_int, (ctypes.POINTER(QikSlabStoreArgs), ctypes.POINTER(ctypes.c_int64))),
     ("qik_slab_store_ws", ctypes.c_int,
      (ctypes.POINTER(QikSlabStoreArgs), ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p)),
+    ("qik_fp8_quant_workspace_size", ctypes.c_int,
+     (ctypes.POINTER(QikFp8QuantArgs), ctypes.POINTER(ctypes.c_int64))),
+    ("qik_fp8_quantize", ctypes.c_int,
+     (ctypes.POINTER(QikFp8QuantArgs), ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p)),
+    ("qik_fp8_gemm_validate", ctypes.c_int, (ctypes.POINTER(QikFp8GemmArgs),)),
+    ("qik_fp8_gemm", ctypes.c_int, (ctypes.POINTER(QikFp8GemmArgs), ctypes.c_void_p)),
+    ("qik_fp8_dequant", ctypes.c_int,
+     (ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p)),
 )
 
 _lock = threading.Lock()

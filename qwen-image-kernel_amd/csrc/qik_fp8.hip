@@ -1,0 +1,762 @@
+// W8A8 fp8 linear of a Qwen-Image 2.1 DiT layer on MI355X (gfx950, CDNA4):
+// per-tensor quantisation of the activation (qwen_image_kernel/fp8.py:24-53)
+// and of a weight (fp8.py:56-60), the fp8 GEMM with tensorwise scales that
+// replaces torch._scaled_mm (fp8.py:87-88), and the weight dequantisation of
+// the bf16 path for layers with fewer than 256 inputs (fp8.py:79-84).
+//
+// The quantiser is an HBM-bound two-pass byte mover (max |x| per block into a
+// small workspace, then every block re-reduces those maxima, forms the scale
+// and writes the codes).  Contraction is off in it, so every fp32 multiply
+// and division rounds on its own, as torch's elementwise ops do.
+//
+// The GEMM runs on the gfx950 fp8 matrix cores: v_mfma_f32_32x32x64_f8f6f4
+// (e4m3 x e4m3, fp32 accumulate; 32x32 outputs x 64 k per instruction, twice
+// the k of the CDNA3 fp8 MFMA).  One workgroup of 4 waves computes a BM x BN
+// tile of out^T = W . A^T (MFMA A operand = weight rows n, B operand =
+// activation rows m), so each lane ends with 4 consecutive n of one row m per
+// register quad and stores 8 contiguous bytes.  Tiles of A and W, 64 k-bytes
+// per stage, reach LDS directly (buffer_load_dwordx4 ... lds, no register
+// staging) NS-1 stages ahead of their use, with a 16-byte chunk swizzle that
+// makes the fragment reads conflict-free; each wave reads the next stage's
+// fragments while its MFMAs run on the current one, and the copies are issued
+// between the MFMAs.  Workgroups map to tiles XCD by XCD (the dispatcher deals
+// workgroup b to XCD b % 8), so one XCD's L2 serves a compact block of tiles.
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string.h>
+#include <limits.h>
+#include <algorithm>
+
+#include "qik_fp8.h"
+
+namespace qik_fp8 {
+
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((__vector_size__(2 * sizeof(__bf16))));
+typedef _Float16 f16x2 __attribute__((__vector_size__(2 * sizeof(_Float16))));
+
+inline bool aligned_to(const void* ptr, uintptr_t a) { return (reinterpret_cast<uintptr_t>(ptr) % a) == 0; }
+
+// CUs of the current device (0 if the runtime cannot say), cached per device
+int device_cus() {
+  static int cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (dev >= 0 && dev < 64) {
+    const int c = __atomic_load_n(&cache[dev], __ATOMIC_RELAXED);
+    if (c > 0) return c;
+  }
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  if (dev >= 0 && dev < 64) __atomic_store_n(&cache[dev], cus, __ATOMIC_RELAXED);
+  return cus;
+}
+
+// ---------------------------------------------------------------------------
+// Quantiser
+// ---------------------------------------------------------------------------
+
+constexpr int QT = 256;          // threads per block
+constexpr int QU = 4;            // 16-byte vectors per thread in flight
+constexpr int MAX_PARTS = 1024;  // blocks of the maximum pass = workspace words
+
+struct QuantParams {
+  const char* x;
+  unsigned char* out;
+  float* scale;
+  unsigned* part;  // [nparts] max |x| of each block's share, as fp32 bit patterns
+  int64_t n;       // elements
+  int64_t nvec;    // whole 16-byte vectors of x
+  int nparts;
+};
+
+template <int DT>
+struct Elem;
+template <>
+struct Elem<QIK_DTYPE_BF16> {
+  static constexpr int PER_VEC = 8;
+  __device__ static float get(const char* x, int64_t i) {
+    return __uint_as_float((unsigned)reinterpret_cast<const unsigned short*>(x)[i] << 16);
+  }
+  __device__ static void unpack(const u32x4 v, float (&f)[8]) {
+    const unsigned w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[2 * i] = __uint_as_float(w[i] << 16);
+      f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  }
+};
+template <>
+struct Elem<QIK_DTYPE_FP16> {
+  static constexpr int PER_VEC = 8;
+  __device__ static float get(const char* x, int64_t i) { return (float)reinterpret_cast<const _Float16*>(x)[i]; }
+  __device__ static void unpack(const u32x4 v, float (&f)[8]) {
+    const unsigned w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f16x2 h = __builtin_bit_cast(f16x2, w[i]);
+      f[2 * i] = (float)h[0];
+      f[2 * i + 1] = (float)h[1];
+    }
+  }
+};
+template <>
+struct Elem<QIK_DTYPE_FP32> {
+  static constexpr int PER_VEC = 4;
+  __device__ static float get(const char* x, int64_t i) { return reinterpret_cast<const float*>(x)[i]; }
+  __device__ static void unpack(const u32x4 v, float (&f)[4]) {
+    f[0] = __uint_as_float(v.x);
+    f[1] = __uint_as_float(v.y);
+    f[2] = __uint_as_float(v.z);
+    f[3] = __uint_as_float(v.w);
+  }
+};
+
+// |x| as an fp32 bit pattern: unsigned order = |x| order, with every NaN above
+// +inf, so an integer max propagates NaN like torch's amax does
+__device__ __forceinline__ unsigned abs_bits(float f) { return __float_as_uint(f) & 0x7fffffffu; }
+
+// max over the block of v (valid in thread 0)
+__device__ __forceinline__ unsigned block_max(unsigned v) {
+  __shared__ unsigned red[QT / 64];
+#pragma unroll
+  for (int k = 32; k >= 1; k >>= 1) v = max(v, (unsigned)__shfl_xor((int)v, k));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int i = 1; i < QT / 64; ++i) v = max(v, red[i]);
+  }
+  return v;
+}
+
+// Block b: max |x| over vectors [b*nvec/nparts, (b+1)*nvec/nparts); the last
+// block also covers the elements past the last whole vector.
+template <int DT>
+__global__ void __launch_bounds__(QT) amax_kernel(const QuantParams p) {
+  using E = Elem<DT>;
+  const int64_t v0 = p.nvec * blockIdx.x / p.nparts;
+  const int64_t v1 = p.nvec * (blockIdx.x + 1) / p.nparts;
+  const u32x4* src = reinterpret_cast<const u32x4*>(p.x);
+  unsigned m = 0;
+  for (int64_t v = v0 + threadIdx.x; v < v1; v += QT * QU) {
+    u32x4 raw[QU];
+#pragma unroll
+    for (int u = 0; u < QU; ++u) raw[u] = (v + u * QT < v1) ? src[v + u * QT] : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int u = 0; u < QU; ++u) {
+      float f[E::PER_VEC];
+      E::unpack(raw[u], f);
+#pragma unroll
+      for (int i = 0; i < E::PER_VEC; ++i) m = max(m, abs_bits(f[i]));
+    }
+  }
+  if (blockIdx.x == gridDim.x - 1) {
+    for (int64_t i = p.nvec * E::PER_VEC + threadIdx.x; i < p.n; i += QT) m = max(m, abs_bits(E::get(p.x, i)));
+  }
+  m = block_max(m);
+  if (threadIdx.x == 0) p.part[blockIdx.x] = m;
+}
+
+// amax -> scale = max(amax * fp32(1/448), 1e-12) (NaN stays NaN: fmaxf would drop it)
+__device__ __forceinline__ float scale_of(unsigned amax_bits) {
+#pragma clang fp contract(off)
+  const float amax = __uint_as_float(amax_bits);
+  if (amax != amax) return amax;
+  return fmaxf(amax * (1.0f / 448.0f), 1e-12f);
+}
+
+// two fp32 values -> two e4m3fn codes (round to nearest even), as 16 bits
+__device__ __forceinline__ unsigned cvt2(float a, float b) {
+  return (unsigned)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false) & 0xffffu;
+}
+
+template <int MODE>
+__device__ __forceinline__ float quant_value(float x, float scale, float inv) {
+#pragma clang fp contract(off)
+  if constexpr (MODE == QIK_FP8_ACTIVATION) {
+    return x * inv;
+  } else {
+    return fminf(fmaxf(x / scale, -448.0f), 448.0f);
+  }
+}
+
+// Every block reduces the partial maxima to the scale (block 0 stores it),
+// then writes the codes of vectors [blockIdx*QT*QU, (blockIdx+1)*QT*QU); the
+// last block also codes the elements past the last whole vector.
+template <int DT, int MODE>
+__global__ void __launch_bounds__(QT) cast_kernel(const QuantParams p) {
+#pragma clang fp contract(off)
+  using E = Elem<DT>;
+  constexpr int PV = E::PER_VEC;
+  const int64_t vbase = (int64_t)blockIdx.x * QT * QU + threadIdx.x;
+  const u32x4* src = reinterpret_cast<const u32x4*>(p.x);
+  u32x4 raw[QU];
+#pragma unroll
+  for (int u = 0; u < QU; ++u) raw[u] = (vbase + u * QT < p.nvec) ? src[vbase + u * QT] : u32x4{0u, 0u, 0u, 0u};
+
+  unsigned m = 0;
+  for (int i = threadIdx.x; i < p.nparts; i += QT) m = max(m, p.part[i]);
+  m = block_max(m);
+  __shared__ float sh_scale;
+  if (threadIdx.x == 0) {
+    sh_scale = scale_of(m);
+    if (blockIdx.x == 0) p.scale[0] = sh_scale;
+  }
+  __syncthreads();
+  const float scale = sh_scale;
+  const float inv = 1.0f / scale;  // IEEE division (the reference's cast kernel: 1.0 / scale)
+
+#pragma unroll
+  for (int u = 0; u < QU; ++u) {
+    const int64_t v = vbase + u * QT;
+    if (v >= p.nvec) continue;
+    float f[PV];
+    E::unpack(raw[u], f);
+    if constexpr (PV == 8) {
+      u32x2 o;
+      o.x = cvt2(quant_value<MODE>(f[0], scale, inv), quant_value<MODE>(f[1], scale, inv)) |
+            (cvt2(quant_value<MODE>(f[2], scale, inv), quant_value<MODE>(f[3], scale, inv)) << 16);
+      o.y = cvt2(quant_value<MODE>(f[4], scale, inv), quant_value<MODE>(f[5], scale, inv)) |
+            (cvt2(quant_value<MODE>(f[6], scale, inv), quant_value<MODE>(f[7], scale, inv)) << 16);
+      reinterpret_cast<u32x2*>(p.out)[v] = o;
+    } else {
+      reinterpret_cast<unsigned*>(p.out)[v] =
+          cvt2(quant_value<MODE>(f[0], scale, inv), quant_value<MODE>(f[1], scale, inv)) |
+          (cvt2(quant_value<MODE>(f[2], scale, inv), quant_value<MODE>(f[3], scale, inv)) << 16);
+    }
+  }
+  if (blockIdx.x == gridDim.x - 1) {
+    for (int64_t i = p.nvec * PV + threadIdx.x; i < p.n; i += QT)
+      p.out[i] = (unsigned char)cvt2(quant_value<MODE>(E::get(p.x, i), scale, inv), 0.0f);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Dequantiser (the bf16 path's weight)
+// ---------------------------------------------------------------------------
+
+template <bool FP16>
+__device__ __forceinline__ unsigned pack2(float a, float b) {  // round to nearest even
+  if constexpr (FP16) {
+    const f16x2 h = {(_Float16)a, (_Float16)b};
+    return __builtin_bit_cast(unsigned, h);
+  } else {
+    const bf16x2 h = {(__bf16)a, (__bf16)b};
+    return __builtin_bit_cast(unsigned, h);
+  }
+}
+
+template <bool FP16>
+__device__ __forceinline__ void unpack2(unsigned w, float& a, float& b) {
+  if constexpr (FP16) {
+    const f16x2 h = __builtin_bit_cast(f16x2, w);
+    a = (float)h[0];
+    b = (float)h[1];
+  } else {
+    a = __uint_as_float(w << 16);
+    b = __uint_as_float(w & 0xffff0000u);
+  }
+}
+
+// fp32 value of an e4m3fn code pair (bytes 2*hi, 2*hi+1 of w): exact
+template <bool HI>
+__device__ __forceinline__ f32x2 decode2(unsigned w) {
+  return __builtin_amdgcn_cvt_pk_f32_fp8((int)w, HI);
+}
+
+template <bool FP16>
+__global__ void __launch_bounds__(QT) dequant_kernel(const unsigned char* w, const float* scale, char* out,
+                                                      int64_t n) {
+#pragma clang fp contract(off)
+  const float s = scale[0];
+  const int64_t v = (int64_t)blockIdx.x * QT + threadIdx.x;  // 8 codes per thread
+  const int64_t nvec = n / 8;
+  if (v < nvec) {
+    const u32x2 c = reinterpret_cast<const u32x2*>(w)[v];
+    u32x4 o;
+    f32x2 f;
+    // round(fp32(code) * s) in the output type; the empty asm keeps the fp32
+    // product from being folded into a mixed-precision fma that rounds once
+    f = decode2<false>(c.x); f[0] *= s; f[1] *= s; asm volatile("" : "+v"(f)); o.x = pack2<FP16>(f[0], f[1]);
+    f = decode2<true>(c.x);  f[0] *= s; f[1] *= s; asm volatile("" : "+v"(f)); o.y = pack2<FP16>(f[0], f[1]);
+    f = decode2<false>(c.y); f[0] *= s; f[1] *= s; asm volatile("" : "+v"(f)); o.z = pack2<FP16>(f[0], f[1]);
+    f = decode2<true>(c.y);  f[0] *= s; f[1] *= s; asm volatile("" : "+v"(f)); o.w = pack2<FP16>(f[0], f[1]);
+    reinterpret_cast<u32x4*>(out)[v] = o;
+  }
+  if (v == 0) {
+    for (int64_t i = nvec * 8; i < n; ++i) {
+      f32x2 f = decode2<false>((unsigned)w[i]);
+      f[0] *= s;
+      asm volatile("" : "+v"(f));
+      const unsigned h = pack2<FP16>(f[0], 0.0f);
+      reinterpret_cast<unsigned short*>(out)[i] = (unsigned short)(h & 0xffffu);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// GEMM
+// ---------------------------------------------------------------------------
+
+constexpr int GT = 256;  // threads per GEMM workgroup (4 waves)
+constexpr int KB = 64;   // k bytes per stage (one MFMA k-step)
+
+struct GemmParams {
+  const unsigned char* a;
+  const unsigned char* w;
+  const float* sa;
+  const float* sw;
+  const char* bias;
+  char* out;
+  int M, N, K;
+  int lda, ldw;   // bytes
+  int64_t ldc;    // elements
+  int ntm, ntn;   // tiles along m and n
+  int group_m;    // tile rows per group of the tile order
+};
+
+template <int BM_, int BN_, int NS_>
+struct Cfg {
+  static constexpr int BM = BM_, BN = BN_, NS = NS_;
+  static constexpr int WM = BM / 2, WN = BN / 2;  // wave tile (2 x 2 waves)
+  static constexpr int MI = WM / 32, NJ = WN / 32;
+  static constexpr int A_BYTES = BM * KB;          // A tile of one stage
+  static constexpr int STAGE = (BM + BN) * KB;
+  static constexpr int AI = BM / 64;               // 1 KiB copies of A per wave per stage
+  static constexpr int WI = BN / 64;
+  static constexpr int COPIES = AI + WI;
+  static_assert(BM % 64 == 0 && BN % 64 == 0, "tiles are multiples of 64");
+  static_assert(NS >= 3, "copies run at least two stages ahead");
+};
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+// 64 lanes x 16 B global -> LDS (buffer_load_dwordx4 ... lds): lane l's 16
+// bytes land at LDS byte lds_addr + 16*l.  Asm, so the compiler neither moves
+// the fragment reads around it nor waits for it; the main loop waits for the
+// copies itself (vmcnt) before the barrier that publishes a stage.
+__device__ __forceinline__ void dma16(u32x4 rsrc, uint32_t lds_addr, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :: "s"(lds_addr), "v"(voff), "s"(rsrc) : "m0");
+}
+#pragma clang diagnostic pop
+
+// Wave-uniform buffer resource over [base, base + bytes): loads at or past
+// `bytes` return zeros.
+__device__ __forceinline__ u32x4 rsrc_words(const unsigned char* base, uint32_t bytes) {
+  const uint64_t a = (uint64_t)(uintptr_t)base;
+  return u32x4{(uint32_t)a, (uint32_t)(a >> 32) & 0xffffu, bytes, 0x00020000u};
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt field");
+  // vmcnt in bits 3:0 and 15:14, expcnt (7) and lgkmcnt (63) left alone
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0x3f << 8));
+}
+
+// Layout of a stage in LDS: A rows [BM][64 B], then W rows [BN][64 B].  The
+// 16-byte chunk c of row r sits at physical chunk c ^ ((r >> 2) & 3): a
+// fragment read (32 rows, one chunk each per 32 lanes) then touches all 64
+// banks once per 16 lanes, and a 1 KiB copy (16 rows x 4 chunks) writes one
+// contiguous KiB.
+__device__ __forceinline__ int swz(int r) { return (r >> 2) & 3; }
+
+template <class C, bool FP16>
+__global__ void __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(1, 1)))
+fp8_gemm_kernel(const GemmParams p) {
+  __shared__ __attribute__((aligned(1024))) unsigned char lds[C::NS * C::STAGE];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: copy targets go to SGPRs
+  const int wm = wave & 1, wn = wave >> 1;
+
+  // tile of this workgroup: XCD x = blockIdx % 8 takes a contiguous run of
+  // the tile order, which walks group_m tile rows at a time
+  const int T = p.ntm * p.ntn;
+  const int bx = blockIdx.x;
+  const int x = bx & 7, s = bx >> 3;
+  const int q = T >> 3, r = T & 7;
+  const int t = x * q + min(x, r) + s;
+  const int gsz_full = p.group_m * p.ntn;
+  const int g = t / gsz_full;
+  const int first = g * p.group_m;
+  const int gm = min(p.group_m, p.ntm - first);
+  const int tr = t - g * gsz_full;
+  const int tm = first + tr % gm;
+  const int tn = tr / gm;
+  const int m0 = tm * C::BM, n0 = tn * C::BN;
+  const int mrows = min(C::BM, p.M - m0);
+  const int nrows = min(C::BN, p.N - n0);
+
+  // per-lane copy offsets: copy i of this wave fills 16-row group wave + 4 i
+  // of its tile; lane l writes row l/4 of the group, physical chunk l%4,
+  // which holds logical chunk (l%4) ^ swz(row)
+  const int crow = wave * 16 + (lane >> 2);
+  const int cchunk = ((lane & 3) ^ ((lane >> 4) & 3)) * 16;
+  uint32_t aoff[C::AI], woff[C::WI];
+#pragma unroll
+  for (int i = 0; i < C::AI; ++i) aoff[i] = (uint32_t)((crow + 64 * i) * p.lda + cchunk);
+#pragma unroll
+  for (int i = 0; i < C::WI; ++i) woff[i] = (uint32_t)((crow + 64 * i) * p.ldw + cchunk);
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_ptr_t)lds;
+  const unsigned char* abase = p.a + (int64_t)m0 * p.lda;
+  const unsigned char* wbase = p.w + (int64_t)n0 * p.ldw;
+  const int nk = (p.K + KB - 1) / KB;
+
+  // copy state of one k-step: the stage's LDS address and the two buffer
+  // resources; past the end of K a lane's chunk would read the next row, so
+  // its offset gets the top bit (out of range: it lands as zeros)
+  struct StepCopies {
+    u32x4 ra, rw;
+    uint32_t st;
+    uint32_t dead;  // 0, or 0x80000000 for a lane whose chunk lies past K
+  };
+  // A k-step at or past the end (kt >= nk) gets empty resources: its copies
+  // fetch nothing and write zeros into a stage that no later step reads, so
+  // every step issues the same copies and the vmcnt waits stay uniform.
+  auto prepare = [&](const int kt) __attribute__((always_inline)) {
+    StepCopies sc;
+    const int koff = kt * KB;
+    const int lim = p.K - koff;  // k bytes left in every row
+    const int kin = min(KB, lim);
+    sc.ra = rsrc_words(abase + koff, kt < nk ? (uint32_t)((mrows - 1) * p.lda + kin) : 0u);
+    sc.rw = rsrc_words(wbase + koff, kt < nk ? (uint32_t)((nrows - 1) * p.ldw + kin) : 0u);
+    sc.st = lds0 + (uint32_t)((kt % C::NS) * C::STAGE);
+    sc.dead = (lim < KB && cchunk >= lim) ? 0x80000000u : 0u;
+    return sc;
+  };
+  // copy i of this wave's list (A copies first, then W)
+  auto issue = [&](const StepCopies& sc, const int i) __attribute__((always_inline)) {
+    if (i < C::AI) dma16(sc.ra, sc.st + (uint32_t)((wave + 4 * i) * 1024), aoff[i] | sc.dead);
+    else dma16(sc.rw, sc.st + (uint32_t)(C::A_BYTES + (wave + 4 * (i - C::AI)) * 1024), woff[i - C::AI] | sc.dead);
+  };
+  auto copy_stage = [&](const int kt) __attribute__((always_inline)) {
+    const StepCopies sc = prepare(kt);
+#pragma unroll
+    for (int i = 0; i < C::COPIES; ++i) issue(sc, i);
+  };
+
+  // fragment read offsets: lane l reads row l%32 of a 32-row block, logical
+  // chunks 2*(l/32) and 2*(l/32)+1
+  const int frow = lane & 31;
+  const uint32_t f0 = (uint32_t)(frow * KB + (((lane >> 5) * 2) ^ swz(frow)) * 16);
+  const uint32_t f1 = (uint32_t)(frow * KB + (((lane >> 5) * 2 + 1) ^ swz(frow)) * 16);
+  auto read_frags = [&](const int kt, i32x8 (&fa)[C::MI], i32x8 (&fw)[C::NJ]) __attribute__((always_inline)) {
+    const unsigned char* st = lds + (kt % C::NS) * C::STAGE;
+#pragma unroll
+    for (int i = 0; i < C::MI; ++i) {
+      const unsigned char* b = st + (wm * C::WM + i * 32) * KB;
+      const u32x4 lo = *reinterpret_cast<const u32x4*>(b + f0);
+      const u32x4 hi = *reinterpret_cast<const u32x4*>(b + f1);
+      fa[i] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+    }
+#pragma unroll
+    for (int j = 0; j < C::NJ; ++j) {
+      const unsigned char* b = st + C::A_BYTES + (wn * C::WN + j * 32) * KB;
+      const u32x4 lo = *reinterpret_cast<const u32x4*>(b + f0);
+      const u32x4 hi = *reinterpret_cast<const u32x4*>(b + f1);
+      fw[j] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+    }
+  };
+
+  f32x16 acc[C::NJ][C::MI];
+#pragma unroll
+  for (int j = 0; j < C::NJ; ++j)
+#pragma unroll
+    for (int i = 0; i < C::MI; ++i) acc[j][i] = f32x16{};
+
+  // prologue: stages 0 .. NS-2 in flight, stage 0 published, its fragments read
+#pragma unroll
+  for (int s0 = 0; s0 < C::NS - 1; ++s0) copy_stage(s0);
+  wait_vmcnt<(C::NS - 2) * C::COPIES>();
+  __syncthreads();
+  i32x8 fa[2][C::MI], fw[2][C::NJ];
+  read_frags(0, fa[0], fw[0]);
+
+  // k-step kt: publish stage kt+1 (its copies done, and every wave past its
+  // MFMAs of kt-1, so stage kt-1 = kt+NS-1 is free), read its fragments,
+  // then run the MFMAs of kt with the copies of kt+NS-1 between them
+  // (sched_barrier(0) pins: the compiler would otherwise hoist the wait and
+  // barrier of the next step above this step's MFMAs, exposing the copies'
+  // whole latency, and bunch the copies together)
+  auto step = [&](const int kt, const int cur) __attribute__((always_inline)) {
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vmcnt<(C::NS - 3) * C::COPIES>();
+    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+    if (kt + 1 < nk) read_frags(kt + 1, fa[cur ^ 1], fw[cur ^ 1]);
+    constexpr int NMF = C::NJ * C::MI;
+    const StepCopies sc = prepare(kt + C::NS - 1);
+#pragma unroll
+    for (int idx = 0; idx < NMF; ++idx) {
+      const int j = idx / C::MI, i = idx % C::MI;
+      acc[j][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fw[cur][j], fa[cur][i], acc[j][i], 0, 0, 0, 0,
+                                                                   0, 0);
+      // this wave's copies spread evenly over the MFMAs
+#pragma unroll
+      for (int c = idx * C::COPIES / NMF; c < (idx + 1) * C::COPIES / NMF; ++c) {
+        __builtin_amdgcn_sched_barrier(0);
+        issue(sc, c);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  };
+  int kt = 0;
+  for (; kt + 1 < nk; kt += 2) {
+    step(kt, 0);
+    step(kt + 1, 1);
+  }
+  if (kt < nk) step(kt, 0);
+
+  // epilogue: out[m][n..n+3] = round(acc * (sa * sw) + bias[n..n+3])
+  {
+#pragma clang fp contract(off)
+    const float ab = p.sa[0] * p.sw[0];
+#pragma unroll
+    for (int j = 0; j < C::NJ; ++j) {
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd) {
+        const int n = n0 + wn * C::WN + j * 32 + qd * 8 + (lane >> 5) * 4;
+        if (n >= p.N) continue;
+        float bv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (p.bias != nullptr) {
+          const u32x2 braw = *reinterpret_cast<const u32x2*>(p.bias + (int64_t)n * 2);
+          unpack2<FP16>(braw.x, bv[0], bv[1]);
+          unpack2<FP16>(braw.y, bv[2], bv[3]);
+        }
+#pragma unroll
+        for (int i = 0; i < C::MI; ++i) {
+          const int m = m0 + wm * C::WM + i * 32 + (lane & 31);
+          if (m >= p.M) continue;
+          float y[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            y[e] = acc[j][i][qd * 4 + e] * ab;
+            y[e] = y[e] + bv[e];
+          }
+          const u32x2 o = {pack2<FP16>(y[0], y[1]), pack2<FP16>(y[2], y[3])};
+          *reinterpret_cast<u32x2*>(p.out + (m * p.ldc + n) * 2) = o;
+        }
+      }
+    }
+  }
+}
+
+}  // namespace qik_fp8
+
+namespace qik_fp8 {
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+
+int validate_quant(const qik_fp8_quant_args* a) {
+  if (a == nullptr) return QIK_ERR_NULL_ARG;
+  if (a->abi_version != QIK_ABI_VERSION || a->reserved0 != 0) return QIK_ERR_ABI_VERSION;
+  if (a->dtype != QIK_DTYPE_BF16 && a->dtype != QIK_DTYPE_FP16 && a->dtype != QIK_DTYPE_FP32) return QIK_ERR_DTYPE;
+  if (a->mode != QIK_FP8_ACTIVATION && a->mode != QIK_FP8_WEIGHT) return QIK_ERR_DTYPE;
+  if (a->n < 1 || a->n >= ((int64_t)1 << 40)) return QIK_ERR_SHAPE;
+  if (a->x == nullptr || a->out == nullptr || a->scale == nullptr) return QIK_ERR_NULL_ARG;
+  const int per_vec = a->dtype == QIK_DTYPE_FP32 ? 4 : 8;
+  if (!aligned_to(a->x, 16) || !aligned_to(a->out, per_vec) || !aligned_to(a->scale, 4)) return QIK_ERR_ALIGN;
+  return QIK_OK;
+}
+
+// blocks of the maximum pass: about 8 vectors per thread, at most MAX_PARTS
+int quant_parts(const qik_fp8_quant_args* a) {
+  const int per_vec = a->dtype == QIK_DTYPE_FP32 ? 4 : 8;
+  const int64_t nvec = a->n / per_vec;
+  const int64_t parts = (nvec + QT * 8 - 1) / (QT * 8);
+  return (int)std::max<int64_t>(1, std::min<int64_t>(parts, MAX_PARTS));
+}
+
+template <int DT>
+int launch_quant(const qik_fp8_quant_args* a, unsigned* part, hipStream_t s) {
+  constexpr int PV = Elem<DT>::PER_VEC;
+  QuantParams p;
+  memset(&p, 0, sizeof(p));
+  p.x = static_cast<const char*>(a->x);
+  p.out = static_cast<unsigned char*>(a->out);
+  p.scale = a->scale;
+  p.part = part;
+  p.n = a->n;
+  p.nvec = a->n / PV;
+  p.nparts = quant_parts(a);
+  void* args[] = {&p};
+  if (hipLaunchKernel((const void*)amax_kernel<DT>, dim3((unsigned)p.nparts), dim3(QT), args, 0, s) != hipSuccess)
+    return QIK_ERR_LAUNCH;
+  const int64_t grid = std::max<int64_t>(1, (p.nvec + QT * QU - 1) / (QT * QU));
+  if (grid > (int64_t)INT_MAX) return QIK_ERR_SHAPE;
+  const void* fn = a->mode == QIK_FP8_ACTIVATION ? (const void*)cast_kernel<DT, QIK_FP8_ACTIVATION>
+                                                 : (const void*)cast_kernel<DT, QIK_FP8_WEIGHT>;
+  return hipLaunchKernel(fn, dim3((unsigned)grid), dim3(QT), args, 0, s) == hipSuccess ? QIK_OK : QIK_ERR_LAUNCH;
+}
+
+// GEMM tile shapes, largest first
+typedef Cfg<256, 256, 4> Cfg256x256;
+typedef Cfg<256, 128, 4> Cfg256x128;
+typedef Cfg<128, 128, 4> Cfg128x128;
+
+struct TileChoice {
+  int bm, bn;
+};
+
+// The tile shape with the shortest estimated makespan on `cus` CUs: a CU's
+// workgroups share its matrix cores, so the makespan is about
+// ceil(tiles / cus) tiles of work per CU, each at the shape's measured rate
+// relative to the 256 x 256 tile.
+TileChoice choose_tile(int64_t M, int64_t N, int cus) {
+  struct Cand {
+    int bm, bn;
+    double rel_rate;
+  };
+  static const Cand cands[] = {{256, 256, 1.0}, {256, 128, 0.9}, {128, 128, 0.75}};
+  if (cus <= 0) cus = 256;
+  TileChoice best = {256, 256};
+  double best_cost = 1e300;
+  for (const Cand& c : cands) {
+    const int64_t tiles = ((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn);
+    const int64_t rounds = (tiles + cus - 1) / cus;
+    const double cost = (double)rounds * c.bm * c.bn / c.rel_rate;
+    if (cost < best_cost * 0.999) {
+      best_cost = cost;
+      best = {c.bm, c.bn};
+    }
+  }
+  return best;
+}
+
+// tile rows per group of the tile order: the group size that minimises the
+// bytes one XCD's run of tiles reads (its distinct A row blocks + W row blocks)
+int choose_group_m(int ntm, int ntn, int bm, int bn) {
+  const int64_t T = (int64_t)ntm * ntn;
+  const int64_t per_xcd = std::max<int64_t>(1, (T + 7) / 8);
+  int best = 1;
+  double best_bytes = 1e300;
+  for (int gm = 1; gm <= std::min(ntm, 16); ++gm) {
+    const int64_t rows = std::min<int64_t>(gm, per_xcd);
+    const int64_t cols = std::min<int64_t>(ntn, (per_xcd + gm - 1) / gm);
+    const double bytes = (double)rows * bm + (double)cols * bn;
+    if (bytes < best_bytes) {
+      best_bytes = bytes;
+      best = gm;
+    }
+  }
+  return best;
+}
+
+template <class C>
+int launch_gemm(GemmParams p, bool fp16, hipStream_t s) {
+  p.ntm = (p.M + C::BM - 1) / C::BM;
+  p.ntn = (p.N + C::BN - 1) / C::BN;
+  p.group_m = choose_group_m(p.ntm, p.ntn, C::BM, C::BN);
+  const int64_t tiles = (int64_t)p.ntm * p.ntn;
+  if (tiles > (int64_t)INT_MAX) return QIK_ERR_SHAPE;
+  void* args[] = {&p};
+  const void* fn = fp16 ? (const void*)fp8_gemm_kernel<C, true> : (const void*)fp8_gemm_kernel<C, false>;
+  return hipLaunchKernel(fn, dim3((unsigned)tiles), dim3(GT), args, 0, s) == hipSuccess ? QIK_OK : QIK_ERR_LAUNCH;
+}
+
+}  // namespace qik_fp8
+
+extern "C" {
+
+int qik_fp8_quant_workspace_size(const qik_fp8_quant_args* a, int64_t* bytes) {
+  if (bytes == nullptr) return QIK_ERR_NULL_ARG;
+  *bytes = 0;
+  const int st = qik_fp8::validate_quant(a);
+  if (st != QIK_OK) return st;
+  *bytes = (int64_t)qik_fp8::quant_parts(a) * (int64_t)sizeof(unsigned);
+  return QIK_OK;
+}
+
+int qik_fp8_quantize(const qik_fp8_quant_args* a, void* workspace, int64_t workspace_bytes, void* stream) {
+  using namespace qik_fp8;
+  const int st = validate_quant(a);
+  if (st != QIK_OK) return st;
+  const int64_t need = (int64_t)quant_parts(a) * (int64_t)sizeof(unsigned);
+  if (workspace == nullptr || workspace_bytes < need || !aligned_to(workspace, 4)) return QIK_ERR_WORKSPACE;
+  unsigned* part = static_cast<unsigned*>(workspace);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (a->dtype) {
+    case QIK_DTYPE_BF16: return launch_quant<QIK_DTYPE_BF16>(a, part, s);
+    case QIK_DTYPE_FP16: return launch_quant<QIK_DTYPE_FP16>(a, part, s);
+    default: return launch_quant<QIK_DTYPE_FP32>(a, part, s);
+  }
+}
+
+int qik_fp8_gemm_validate(const qik_fp8_gemm_args* a) {
+  using namespace qik_fp8;
+  if (a == nullptr) return QIK_ERR_NULL_ARG;
+  if (a->abi_version != QIK_ABI_VERSION || a->reserved0 != 0 || a->reserved1 != 0) return QIK_ERR_ABI_VERSION;
+  if (a->out_dtype != QIK_DTYPE_BF16 && a->out_dtype != QIK_DTYPE_FP16) return QIK_ERR_DTYPE;
+  if (a->M < 1 || a->N < 16 || a->K < 16 || a->N % 16 != 0 || a->K % 16 != 0) return QIK_ERR_SHAPE;
+  if (a->M > (int64_t)INT_MAX || a->N > (int64_t)INT_MAX || a->K > (int64_t)INT_MAX) return QIK_ERR_SHAPE;
+  if (a->lda < a->K || a->ldw < a->K || a->ldc < a->N) return QIK_ERR_SHAPE;
+  // a tile's rows must be addressable by a 31-bit buffer offset
+  if (a->lda > (int64_t)(INT_MAX / 256) || a->ldw > (int64_t)(INT_MAX / 256)) return QIK_ERR_SHAPE;
+  if (a->a == nullptr || a->w == nullptr || a->scale_a == nullptr || a->scale_w == nullptr || a->out == nullptr)
+    return QIK_ERR_NULL_ARG;
+  if (a->lda % 16 != 0 || a->ldw % 16 != 0 || a->ldc % 8 != 0) return QIK_ERR_ALIGN;
+  if (!aligned_to(a->a, 16) || !aligned_to(a->w, 16) || !aligned_to(a->out, 16) || !aligned_to(a->scale_a, 4) ||
+      !aligned_to(a->scale_w, 4))
+    return QIK_ERR_ALIGN;
+  if (a->bias != nullptr && !aligned_to(a->bias, 8)) return QIK_ERR_ALIGN;
+  return QIK_OK;
+}
+
+int qik_fp8_gemm(const qik_fp8_gemm_args* a, void* stream) {
+  using namespace qik_fp8;
+  const int st = qik_fp8_gemm_validate(a);
+  if (st != QIK_OK) return st;
+  GemmParams p;
+  memset(&p, 0, sizeof(p));
+  p.a = static_cast<const unsigned char*>(a->a);
+  p.w = static_cast<const unsigned char*>(a->w);
+  p.sa = a->scale_a;
+  p.sw = a->scale_w;
+  p.bias = static_cast<const char*>(a->bias);
+  p.out = static_cast<char*>(a->out);
+  p.M = (int)a->M;
+  p.N = (int)a->N;
+  p.K = (int)a->K;
+  p.lda = (int)a->lda;
+  p.ldw = (int)a->ldw;
+  p.ldc = a->ldc;
+  const bool fp16 = a->out_dtype == QIK_DTYPE_FP16;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const TileChoice tc = choose_tile(a->M, a->N, device_cus());
+  if (tc.bm == 256 && tc.bn == 256) return launch_gemm<Cfg256x256>(p, fp16, s);
+  if (tc.bm == 256) return launch_gemm<Cfg256x128>(p, fp16, s);
+  return launch_gemm<Cfg128x128>(p, fp16, s);
+}
+
+int qik_fp8_dequant(const void* w, const float* scale, void* out, int64_t n, int32_t out_dtype, void* stream) {
+  using namespace qik_fp8;
+  if (out_dtype != QIK_DTYPE_BF16 && out_dtype != QIK_DTYPE_FP16) return QIK_ERR_DTYPE;
+  if (n < 0 || n / 8 >= (int64_t)INT_MAX * QT) return QIK_ERR_SHAPE;
+  if (n == 0) return QIK_OK;
+  if (w == nullptr || scale == nullptr || out == nullptr) return QIK_ERR_NULL_ARG;
+  if (!aligned_to(w, 8) || !aligned_to(out, 16) || !aligned_to(scale, 4)) return QIK_ERR_ALIGN;
+  const int64_t grid = std::max<int64_t>(1, (n / 8 + QT - 1) / QT);
+  const unsigned char* wp = static_cast<const unsigned char*>(w);
+  char* op = static_cast<char*>(out);
+  void* args[] = {&wp, &scale, &op, &n};
+  const void* fn = out_dtype == QIK_DTYPE_FP16 ? (const void*)dequant_kernel<true> : (const void*)dequant_kernel<false>;
+  return hipLaunchKernel(fn, dim3((unsigned)grid), dim3(QT), args, 0, static_cast<hipStream_t>(stream)) ==
+                 hipSuccess
+             ? QIK_OK
+             : QIK_ERR_LAUNCH;
+}
+
+}  // extern "C"

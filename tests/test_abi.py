@@ -20,7 +20,7 @@ from qwen_image_kernel_amd import _lib, attention
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "qik_attn.h")
-HEADERS = [HEADER, os.path.join(ROOT, "include", "qik_ops.h")]
+HEADERS = [HEADER, os.path.join(ROOT, "include", "qik_ops.h"), os.path.join(ROOT, "include", "qik_fp8.h")]
 
 
 def header_functions():
@@ -48,10 +48,13 @@ def test_library_loads_and_exports_every_declared_symbol():
 
 @pytest.mark.parametrize("cname,pytype", [("qik_attn_args", _lib.QikAttnArgs),
                                            ("qik_rms_rope_args", _lib.QikRmsRopeArgs),
-                                           ("qik_slab_store_args", _lib.QikSlabStoreArgs)])
+                                           ("qik_slab_store_args", _lib.QikSlabStoreArgs),
+                                           ("qik_fp8_quant_args", _lib.QikFp8QuantArgs),
+                                           ("qik_fp8_gemm_args", _lib.QikFp8GemmArgs)])
 def test_struct_layout_matches_c_header(tmp_path, cname, pytype):
     fields = [f for f, _ in pytype._fields_]
-    src = ["#include <stdio.h>", "#include <stddef.h>", '#include "qik_ops.h"', "int main(void) {",
+    src = ["#include <stdio.h>", "#include <stddef.h>", '#include "qik_ops.h"', '#include "qik_fp8.h"',
+           "int main(void) {",
            f'printf("sizeof %zu\\n", sizeof({cname}));']
     for f in fields:
         src.append(f'printf("{f} %zu\\n", offsetof({cname}, {f}));')
@@ -305,3 +308,93 @@ def test_scratch_constant_matches_the_binding():
     text = open(HEADER).read()
     m = re.search(r"#define QIK_ATTN_SCRATCH_BYTES \((\d+) \* 1024 \* 1024\)", text)
     assert int(m.group(1)) * 1024 * 1024 == _lib.ATTN_SCRATCH_BYTES
+
+
+def test_fp8_header_constants_match_the_binding():
+    text = open(os.path.join(ROOT, "include", "qik_fp8.h")).read()
+    assert re.search(r"#define QIK_DTYPE_FP32 (\d+)", text).group(1) == str(_lib.DTYPE_FP32)
+    assert re.search(r"QIK_FP8_ACTIVATION = (\d+)", text).group(1) == str(_lib.FP8_ACTIVATION)
+    assert re.search(r"QIK_FP8_WEIGHT = (\d+)", text).group(1) == str(_lib.FP8_WEIGHT)
+
+
+def _gemm_args(**kw):
+    a = _lib.QikFp8GemmArgs()
+    a.abi_version = _lib.ABI_VERSION
+    a.out_dtype = _lib.DTYPE_BF16
+    a.a, a.w, a.scale_a, a.scale_w, a.out = 0x10000, 0x20000, 0x30000, 0x30004, 0x40000
+    a.M, a.N, a.K = 1536, 4096, 4096
+    a.lda, a.ldw, a.ldc = 4096, 4096, 4096
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize(
+    "kw,code",
+    [
+        ({}, 0),
+        ({"bias": 0x50008}, 0),
+        ({"M": 1, "N": 16, "K": 16, "lda": 16, "ldw": 16, "ldc": 16}, 0),
+        ({"out_dtype": _lib.DTYPE_FP16}, 0),
+        ({"abi_version": 9}, -2),
+        ({"reserved1": 1}, -2),
+        ({"out_dtype": _lib.DTYPE_FP32}, -3),   # fp32 out is not an output type here
+        ({"M": 0}, -5),
+        ({"N": 4100, "ldc": 4100}, -5),        # N % 16 (the _scaled_mm contract)
+        ({"K": 4104}, -5),                     # K % 16
+        ({"lda": 4080}, -5),                   # row stride < K
+        ({"ldc": 4000}, -5),
+        ({"lda": 1 << 24, "ldw": 4096}, -5),   # a tile's rows exceed a 31-bit offset
+        ({"w": None}, -1),
+        ({"scale_a": None}, -1),
+        ({"a": 0x10008}, -8),
+        ({"lda": 4104}, -8),
+        ({"bias": 0x50004}, -8),
+    ],
+)
+def test_fp8_gemm_validate(kw, code):
+    assert _lib.load().qik_fp8_gemm_validate(ctypes.byref(_gemm_args(**kw))) == code
+
+
+def _quant_args(**kw):
+    a = _lib.QikFp8QuantArgs()
+    a.abi_version = _lib.ABI_VERSION
+    a.dtype = _lib.DTYPE_BF16
+    a.mode = _lib.FP8_ACTIVATION
+    a.x, a.out, a.scale = 0x10000, 0x20000, 0x30000
+    a.n = 1536 * 4096
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+def test_fp8_quant_workspace_size_and_checks():
+    lib = _lib.load()
+    n = ctypes.c_int64(-1)
+    assert lib.qik_fp8_quant_workspace_size(ctypes.byref(_quant_args()), ctypes.byref(n)) == 0
+    # one partial maximum per block of 256 threads x 8 vectors, at most 1024
+    assert n.value == 4 * min(1024, -(-(1536 * 4096 // 8) // 2048))
+    assert lib.qik_fp8_quant_workspace_size(ctypes.byref(_quant_args(n=3)), ctypes.byref(n)) == 0
+    assert n.value == 4
+    assert lib.qik_fp8_quant_workspace_size(ctypes.byref(_quant_args(n=1 << 36)), ctypes.byref(n)) == 0
+    assert n.value == 4 * 1024
+    for kw, code in [({"n": 0}, -5), ({"dtype": 5}, -3), ({"mode": 2}, -3), ({"x": None}, -1),
+                     ({"x": 0x10008}, -8), ({"out": 0x20004}, -8), ({"dtype": _lib.DTYPE_FP32, "out": 0x20004}, 0),
+                     ({"reserved0": 1}, -2)]:
+        assert lib.qik_fp8_quant_workspace_size(ctypes.byref(_quant_args(**kw)), ctypes.byref(n)) == code, kw
+    buf = (ctypes.c_uint32 * 1024)()
+    base = ctypes.addressof(buf)
+    WS = -12
+    assert lib.qik_fp8_quantize(ctypes.byref(_quant_args()), None, 4096, None) == WS
+    assert lib.qik_fp8_quantize(ctypes.byref(_quant_args()), base, 4, None) == WS
+    assert lib.qik_fp8_quantize(ctypes.byref(_quant_args()), base + 2, 4096, None) == WS
+
+
+def test_fp8_dequant_rejects_before_any_launch():
+    lib = _lib.load()
+    assert lib.qik_fp8_dequant(0x10000, 0x20000, 0x30000, 64, _lib.DTYPE_FP32, None) == -3
+    assert lib.qik_fp8_dequant(0x10000, 0x20000, 0x30000, -1, _lib.DTYPE_BF16, None) == -5
+    assert lib.qik_fp8_dequant(0x10000, 0x20000, 0x30000, 0, _lib.DTYPE_BF16, None) == 0   # no work
+    assert lib.qik_fp8_dequant(None, 0x20000, 0x30000, 64, _lib.DTYPE_BF16, None) == -1
+    assert lib.qik_fp8_dequant(0x10004, 0x20000, 0x30000, 64, _lib.DTYPE_BF16, None) == -8
+    assert lib.qik_fp8_dequant(0x10000, 0x20000, 0x30008, 64, _lib.DTYPE_BF16, None) == -8

@@ -1,0 +1,313 @@
+"""W8A8 fp8 linear on the GPU: quantiser, GEMM, dequantiser and FP8Linear.
+
+The quantiser must match torch's ops on the same device bit for bit (the
+reference computes the scale with torch ops and casts with one correctly
+rounded reciprocal, fp8.py:24-60), and the oracle's CPU restatement.  The GEMM
+is checked against the fp64 value of the dequantised product (oracle.fp8.scaled_mm,
+or an fp32 torch matmul of the dequantised operands at large sizes) to within
+one bf16 rounding plus the fp32 accumulation error, and against the unquantised
+fp32 product at the reference test's relative-error bar (tests/test_fp8.py:16-30).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import fp8 as of
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda", 0)
+
+
+@pytest.fixture(scope="module")
+def qik():
+    if not torch.cuda.is_available():
+        pytest.skip("needs a HIP device")
+    import qwen_image_kernel_amd as m
+    return m
+
+
+def torch_act_quant(x):
+    """The reference's activation quantisation with torch ops on the device
+    (fp8.py:24-26 for the scale; fp8.py:37-40 for the cast: one reciprocal)."""
+    s = (x.abs().amax().float() / 448.0).clamp_min(1e-12)
+    return (x.float() * (1.0 / s)).to(torch.float8_e4m3fn), s.reshape(1)
+
+
+def torch_weight_quant(w):
+    """fp8.py:56-60 verbatim in torch ops on the device."""
+    s = (w.abs().amax().float() / 448.0).clamp_min(1e-12)
+    return (w.float() / s).clamp(-448.0, 448.0).to(torch.float8_e4m3fn), s.reshape(1)
+
+
+def codes(t):
+    return t.view(torch.uint8).cpu().numpy()
+
+
+def _inputs(shape, dtype, seed, kind="normal"):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(*shape, generator=g)
+    if kind == "outlier":
+        x.view(-1)[len(x.view(-1)) // 3] = 3e4
+    elif kind == "tiny":
+        x = x * 1e-20
+    elif kind == "zero":
+        x = torch.zeros(*shape)
+    elif kind == "wide":
+        x = x * torch.exp2(torch.randint(-20, 20, shape, generator=g).float())
+    return x.to(dtype).to(DEV)
+
+
+@pytest.mark.parametrize("shape,dtype,kind", [
+    ((1536, 4096), torch.bfloat16, "normal"),
+    ((4352, 3072), torch.bfloat16, "wide"),
+    ((1, 1), torch.bfloat16, "normal"),
+    ((7,), torch.bfloat16, "normal"),
+    ((1000003,), torch.bfloat16, "outlier"),
+    ((333, 257), torch.float16, "normal"),
+    ((4096, 64), torch.float32, "wide"),
+    ((129, 31), torch.float32, "normal"),
+    ((64, 256), torch.bfloat16, "tiny"),
+    ((64, 256), torch.bfloat16, "zero"),
+])
+@pytest.mark.parametrize("which", ["activation", "weight"])
+def test_quantiser_bit_exact_vs_torch_ops(qik, shape, dtype, kind, which):
+    x = _inputs(shape, dtype, 11 + len(shape) + shape[0], kind)
+    if which == "activation":
+        got_q, got_s = qik.quantize_tensorwise(x)
+        want_q, want_s = torch_act_quant(x)
+    else:
+        got_q, got_s = qik.quantize_weight_tensorwise(x)
+        want_q, want_s = torch_weight_quant(x)
+    assert got_q.shape == x.shape and got_q.dtype == torch.float8_e4m3fn
+    assert got_s.shape == (1,) and got_s.dtype == torch.float32
+    np.testing.assert_array_equal(got_s.cpu().numpy(), want_s.cpu().numpy())
+    np.testing.assert_array_equal(codes(got_q), codes(want_q))
+    if x.numel() <= 1 << 20:
+        oq, osc = (of.quantize_tensorwise if which == "activation" else of.quantize_weight_tensorwise)(
+            x.float().cpu().numpy())
+        assert np.float32(got_s.item()) == osc
+        np.testing.assert_array_equal(codes(got_q), oq)
+
+
+def test_quantiser_strided_and_misaligned_input(qik):
+    base = _inputs((1537, 4096), torch.bfloat16, 5)
+    x = base[1:]               # storage offset of one row: still 16-byte aligned
+    y = base[:, 1:4001]        # strided rows: copied first
+    z = base.view(-1)[3:1003]  # 6-byte offset: copied to an aligned buffer first
+    for t in (x, y, z):
+        got_q, got_s = qik.quantize_tensorwise(t)
+        want_q, want_s = torch_act_quant(t)
+        assert got_s.item() == want_s.item()
+        np.testing.assert_array_equal(codes(got_q), codes(want_q))
+
+
+def test_quantiser_nan_poisons_the_scale(qik):
+    x = _inputs((64, 256), torch.bfloat16, 3)
+    x[5, 7] = float("nan")
+    q, s = qik.quantize_tensorwise(x)
+    assert torch.isnan(s).all()
+    assert torch.isnan(q.float()).all()
+
+
+def test_dequant_bit_exact(qik):
+    g = torch.Generator().manual_seed(2)
+    raw = torch.randint(0, 256, (1000, 64), generator=g, dtype=torch.uint8)
+    raw[raw == 0x7F] = 0x7E
+    raw[raw == 0xFF] = 0xFE
+    w = raw.view(torch.float8_e4m3fn).to(DEV)
+    s = torch.tensor([0.0123], device=DEV)
+    from qwen_image_kernel_amd.fp8 import _dequant_weight
+    for dt in (torch.bfloat16, torch.float16):
+        got = _dequant_weight(w, s, dt)
+        want = (w.to(torch.bfloat16).float() * s).to(dt)   # fp8.py:81 (then .to(x.dtype))
+        np.testing.assert_array_equal(got.view(torch.int16).cpu().numpy(), want.view(torch.int16).cpu().numpy())
+    odd = w.reshape(-1)[:1003]
+    got = _dequant_weight(odd, s, torch.bfloat16)
+    want = (odd.to(torch.bfloat16).float() * s).to(torch.bfloat16)
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
+def _gemm_operands(M, N, K, seed, lda=None):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, K, generator=g)
+    w = torch.randn(N, K, generator=g) * 0.02
+    xq, sx = of.quantize_tensorwise(x.numpy())
+    wq, sw = of.quantize_weight_tensorwise(w.numpy())
+    a = torch.from_numpy(xq).view(torch.float8_e4m3fn)
+    if lda is not None:
+        buf = torch.zeros(M, lda, dtype=torch.uint8)
+        buf[:, :K] = torch.from_numpy(xq)
+        a = buf.view(torch.float8_e4m3fn).to(DEV)[:, :K]
+    else:
+        a = a.to(DEV)
+    return a, torch.from_numpy(wq).view(torch.float8_e4m3fn).to(DEV), xq, wq, np.float32(sx), np.float32(sw)
+
+
+def _half_ulp(v, dtype):
+    """half the spacing of `dtype` (bf16 / fp16) at |v| (normal range)."""
+    mant = 7 if dtype == torch.bfloat16 else 10
+    e = np.floor(np.log2(np.maximum(np.abs(v), 2.0 ** -100)))
+    return 2.0 ** (e - mant - 1)
+
+
+def _check_close(out, ref, abs_sum):
+    """out = round(y) with y the kernel's fp32 result; ref the fp64 value.
+    |y - ref| <= acc := 2^-16 * sum_k |A[m,k] W[n,k]| * scales + |bias|: the
+    fp8 matrix cores sum each block of 64 products in their own way (not an
+    IEEE fp32 loop: the kernel matches hipBLASLt's fp8 GEMM bit for bit, not a
+    sequential fp32 sum; the largest error seen is about 2^-18 of the sum),
+    then the fp32 accumulation, scale and bias steps.  So |out - ref| <= half an
+    output ulp at |ref| + acc, + acc."""
+    o = out.double().cpu().numpy()
+    acc = 2.0 ** -16 * abs_sum
+    bound = _half_ulp(np.abs(ref) + acc, out.dtype) + 2 * acc
+    err = np.abs(o - ref)
+    bad = err > bound
+    if bad.any():
+        i = np.unravel_index(np.argmax(err / bound), err.shape)
+        raise AssertionError(f"{bad.sum()} of {err.size} outside the bound; worst at {i}: out {o[i]!r} "
+                             f"ref {ref[i]!r} err {err[i]:.3g} bound {bound[i]:.3g} acc {acc[i]:.3g}")
+
+
+def _abs_sum(xq, wq, sx, sw, bias):
+    """sum_k |A W| * scales + |bias| per output, the magnitude the rounding errors scale with."""
+    av = torch.from_numpy(np.abs(of.decode(xq))).double()
+    wv = torch.from_numpy(np.abs(of.decode(wq))).double()
+    if torch.cuda.is_available():
+        av, wv = av.to(DEV), wv.to(DEV)
+    s = (av @ wv.T).cpu().numpy() * float(np.float32(sx * sw))
+    return s + (np.abs(bias)[None, :] if bias is not None else 0.0)
+
+
+@pytest.mark.parametrize("M,N,K", [
+    (1536, 4096, 4096),   # 256 x 128 tiles
+    (4352, 3072, 3072),   # 256 x 256 tiles
+    (300, 272, 4096),     # 128 x 128 tiles, ragged M and N
+    (1, 16, 16),
+    (17, 48, 80),         # K tail of 16 bytes
+    (513, 1040, 1104),    # K = 17 * 64 + 16
+    (256, 256, 128),
+])
+@pytest.mark.parametrize("bias", [False, True])
+def test_gemm_vs_fp64_oracle(qik, M, N, K, bias):
+    a, w, xq, wq, sx, sw = _gemm_operands(M, N, K, 1000 + M + N + K)
+    b = torch.randn(N, generator=torch.Generator().manual_seed(9)).to(torch.bfloat16) if bias else None
+    out = qik.fp8_linear(a, w, torch.tensor([sx], device=DEV), torch.tensor([sw], device=DEV),
+                         b.to(DEV) if bias else None)
+    torch.cuda.synchronize()
+    bnp = b.float().numpy() if bias else None
+    if M * N * K <= 1 << 31:
+        ref = of.scaled_mm(xq, wq, sx, sw, bnp)
+    else:
+        av = torch.from_numpy(of.decode(xq)).to(DEV)
+        wv = torch.from_numpy(of.decode(wq)).to(DEV)
+        acc = (av.double() @ wv.double().T)
+        ab = float(np.float32(sx * sw))
+        ref = (acc * ab + (b.to(DEV).double()[None, :] if bias else 0)).cpu().numpy()
+    _check_close(out, ref, _abs_sum(xq, wq, sx, sw, bnp))
+
+
+def test_gemm_fp16_out_and_strided_rows(qik):
+    M, N, K = 640, 512, 1024
+    a, w, xq, wq, sx, sw = _gemm_operands(M, N, K, 77, lda=1040)
+    assert a.stride(0) == 1040
+    b = torch.randn(N, generator=torch.Generator().manual_seed(4)).to(torch.float16)
+    out = qik.fp8_linear(a, w, torch.tensor([sx], device=DEV), torch.tensor([sw], device=DEV), b.to(DEV),
+                         out_dtype=torch.float16)
+    assert out.dtype == torch.float16
+    bnp = b.float().numpy()
+    _check_close(out, of.scaled_mm(xq, wq, sx, sw, bnp), _abs_sum(xq, wq, sx, sw, bnp))
+
+
+@pytest.mark.parametrize("M,K,N,label", [(1536, 4096, 4096, "qkv-like"), (1536, 12288, 4096, "mlp-out-like"),
+                                         (4352, 3072, 3072, "H*D=3072 out"), (4352, 3072, 9216, "H*D=3072 fused qkv")])
+def test_fp8linear_matches_reference_test_bar(qik, M, K, N, label):
+    """tests/test_fp8.py:16-30: FP8Linear.from_linear(nn.Linear * 0.02) within rel-err 0.06 of fp32."""
+    torch.manual_seed(0)
+    lin = torch.nn.Linear(K, N, bias=False, dtype=torch.bfloat16, device=DEV)
+    with torch.no_grad():
+        lin.weight.mul_(0.02)
+    x = torch.randn(M, K, device=DEV, dtype=torch.bfloat16)
+    ref = x.float() @ lin.weight.float().t()
+    fq = qik.FP8Linear.from_linear(lin).to(DEV)
+    out = fq(x)
+    rel = ((out.float() - ref).norm() / ref.norm()).item()
+    assert rel < 0.06, (label, rel)
+    # and tightly against the same computation on the dequantised operands (fp64)
+    xq, s_a = torch_act_quant(x)
+    ab = (s_a * fq.weight_scale).double()
+    dq = (xq.double() @ fq.weight.double().t()) * ab
+    asum = (xq.double().abs() @ fq.weight.double().abs().t()) * ab
+    _check_close(out, dq.cpu().numpy(), asum.cpu().numpy())
+
+
+def test_fp8linear_forward_paths(qik):
+    torch.manual_seed(1)
+    # bias, 3-d input, fp16 activations
+    lin = torch.nn.Linear(512, 768, bias=True, dtype=torch.float16, device=DEV)
+    fq = qik.FP8Linear.from_linear(lin)
+    assert fq.weight.dtype == torch.float8_e4m3fn and fq.bias.dtype == torch.bfloat16
+    x = torch.randn(2, 33, 512, device=DEV, dtype=torch.float16)
+    out = fq(x)
+    assert out.shape == (2, 33, 768) and out.dtype == torch.float16
+    xq, s_a = torch_act_quant(x.reshape(-1, 512))
+    ab = (s_a * fq.weight_scale).double()
+    want = (xq.double() @ fq.weight.double().t()) * ab + fq.bias.double()
+    asum = (xq.double().abs() @ fq.weight.double().abs().t()) * ab + fq.bias.double().abs()
+    # the bf16 result converted to fp16 (exact for these magnitudes)
+    _check_close(out.reshape(-1, 768).to(torch.bfloat16), want.cpu().numpy(), asum.cpu().numpy())
+    # fewer than 256 inputs: the bf16 path on the dequantised weight (fp8.py:79-84)
+    small = torch.nn.Linear(64, 3072, bias=True, dtype=torch.bfloat16, device=DEV)
+    fs = qik.FP8Linear.from_linear(small)
+    x = torch.randn(4, 100, 64, device=DEV, dtype=torch.bfloat16)
+    w = (fs.weight.to(torch.bfloat16).float() * fs.weight_scale).to(torch.bfloat16)
+    want = torch.nn.functional.linear(x, w, fs.bias)
+    assert torch.equal(fs(x), want)
+
+
+def test_from_linear_cpu_weights_match_gpu(qik):
+    torch.manual_seed(2)
+    lin = torch.nn.Linear(1024, 512, bias=True, dtype=torch.bfloat16)
+    fc = qik.FP8Linear.from_linear(lin)
+    assert fc.weight.device.type == "cpu"
+    fg = qik.FP8Linear.from_linear(lin.to(DEV))
+    assert torch.equal(fc.weight.view(torch.uint8), fg.weight.view(torch.uint8).cpu())
+    assert torch.equal(fc.weight_scale, fg.weight_scale.cpu())
+    wq, s = of.quantize_weight_tensorwise(lin.weight.detach().float().cpu().numpy())
+    np.testing.assert_array_equal(fc.weight.view(torch.uint8).numpy(), wq)
+
+
+def test_convert_linears_fp8_and_state_dict(qik):
+    from qwen_image_kernel_amd import fp8 as f8
+    net = torch.nn.Sequential(torch.nn.Linear(256, 256), torch.nn.GELU(),
+                              torch.nn.Sequential(torch.nn.Linear(256, 512, bias=False))).to(DEV)
+    names = f8.convert_linears_fp8(net, skip_patterns=("2.0",))
+    assert names == ["0"]
+    assert isinstance(net[0], f8.FP8Linear) and isinstance(net[2][0], torch.nn.Linear)
+    sd = f8.fp8_state_dict(net)
+    assert sd["0.weight"].dtype == torch.float8_e4m3fn and sd["0.weight_scale"].shape == (1,)
+    assert sd["2.0.weight"].dtype == torch.float32
+
+
+@pytest.mark.parametrize("M,N,K,bias", [(1536, 4096, 4096, False), (4352, 3072, 3072, True),
+                                        (300, 272, 4096, True), (513, 1040, 1104, False)])
+def test_gemm_matches_torch_scaled_mm(qik, M, N, K, bias):
+    """torch._scaled_mm is the call the reference makes (fp8.py:87-88); on this
+    device it is hipBLASLt's fp8 GEMM.  The kernel agrees with it on (almost)
+    every element, and nowhere by more than one bf16 step."""
+    a, w, xq, wq, sx, sw = _gemm_operands(M, N, K, 31 + M + N + K)
+    sa, sb = torch.tensor([sx], device=DEV), torch.tensor([sw], device=DEV)
+    b = (torch.randn(N, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16).to(DEV) if bias else None)
+    try:
+        want = torch._scaled_mm(a, w.t(), scale_a=sa, scale_b=sb, bias=b, out_dtype=torch.bfloat16)
+    except (RuntimeError, NotImplementedError) as e:
+        pytest.skip(f"torch._scaled_mm unavailable here: {e}")
+    got = qik.fp8_linear(a, w, sa, sb, b)
+    same = (got.view(torch.int16) == want.view(torch.int16)).float().mean().item()
+    print(f"M={M} N={N} K={K} bias={bias}: {same:.6f} of the outputs bit-identical to torch._scaled_mm")
+    assert same >= 0.99
+    d = (got.double() - want.double()).abs()
+    step = torch.from_numpy(2 * _half_ulp(want.double().cpu().numpy(), torch.bfloat16)).to(DEV)
+    assert (d <= step).all()

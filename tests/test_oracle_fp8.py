@@ -1,6 +1,7 @@
 """Oracle: fp8e4m3fn / bf16 rounding and the slab quantisation (CPU)."""
 
 import numpy as np
+import pytest
 import torch
 
 from oracle import fp8 as of
@@ -103,3 +104,76 @@ def test_scale_uses_reciprocal_multiply_not_division():
         v[0, 0, 0, 0] = a
         _, scale = of.quantize_per_head(v)
         assert scale[0, 0] == max(a * inv, np.float32(1e-12))
+
+
+# --- W8A8 linear: tensorwise quantisation and the scaled GEMM (fp8.py:24-60, 87-88) ---
+
+
+def test_tensor_scale_known_answers():
+    # all zeros: the clamp (fp8.py:26)
+    assert of.tensor_scale(np.zeros(10, np.float32)) == np.float32(1e-12)
+    # amax * fp32(1/448), not amax / 448 (the GPU's scalar division)
+    x = np.float32([3.0, -7.0, 1.0])
+    assert of.tensor_scale(x) == np.float32(np.float32(7.0) * (np.float32(1.0) / np.float32(448.0)))
+    assert np.isnan(of.tensor_scale(np.float32([1.0, np.nan])))
+
+
+@pytest.mark.parametrize("fn", [of.quantize_tensorwise, of.quantize_weight_tensorwise])
+def test_tensorwise_quant_known_answers(fn):
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal(4096) * 5).astype(np.float32)
+    codes, s = fn(x)
+    # the largest magnitude lands on the largest code
+    i = np.argmax(np.abs(x))
+    assert codes[i] == (0xFE if x[i] < 0 else 0x7E)
+    # representable values times the scale come back as themselves
+    table = of.e4m3fn_decode_table()
+    vals = table[rng.integers(0, 127, 1000)] * rng.choice([-1, 1], 1000)
+    vals[0] = 448.0
+    y = (vals * np.float32(0.37)).astype(np.float32)
+    c, sy = fn(y)
+    np.testing.assert_allclose(of.decode(c) * sy, y, rtol=1e-6)
+    # the codes dequantise to within half an fp8 step of x / scale
+    back = of.decode(codes) * s
+    assert (np.abs(back - x) <= np.abs(x) * 2.0 ** -4 + s * 2.0 ** -10).all()
+
+
+def test_activation_and_weight_forms_differ_only_at_rounding():
+    rng = np.random.default_rng(4)
+    x = (rng.standard_normal(200000)).astype(np.float32)
+    ca, sa = of.quantize_tensorwise(x)
+    cw, sw = of.quantize_weight_tensorwise(x)
+    assert sa == sw
+    diff = ca != cw
+    assert diff.mean() < 1e-3                      # x*(1/s) and x/s differ by an ulp at most
+    assert (np.abs(ca[diff].astype(int) - cw[diff].astype(int)) == 1).all()
+
+
+def test_tensorwise_quant_matches_torch_on_cpu():
+    """The same steps written with torch's CPU ops (the reciprocal of 448 formed
+    explicitly, as the GPU does) give the same codes."""
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal((64, 300)) * 3).astype(np.float32)
+    t = torch.from_numpy(x)
+    s = torch.clamp_min(t.abs().amax() * torch.tensor(1.0 / 448.0, dtype=torch.float32), 1e-12)
+    want = (t * (1.0 / s)).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    got, gs = of.quantize_tensorwise(x)
+    assert np.float32(s.item()) == gs
+    np.testing.assert_array_equal(got, want)
+
+
+def test_scaled_mm_brute_force_and_identity():
+    rng = np.random.default_rng(6)
+    a = rng.integers(0, 127, (5, 48)).astype(np.uint8) | (rng.integers(0, 2, (5, 48)) << 7).astype(np.uint8)
+    w = rng.integers(0, 127, (7, 48)).astype(np.uint8)
+    bias = rng.standard_normal(7).astype(np.float32)
+    got = of.scaled_mm(a, w, 0.5, 0.25, bias)
+    t = of.e4m3fn_decode_table().astype(np.float64)
+    for m in range(5):
+        for n in range(7):
+            s = sum(t[a[m, k]] * t[w[n, k]] for k in range(48))
+            assert got[m, n] == s * 0.125 + np.float64(bias[n])
+    # W = e_k (code of 1.0 at column k): column k of A times the scales
+    eye = np.zeros((48, 48), np.uint8)
+    eye[np.arange(48), np.arange(48)] = 0x38
+    np.testing.assert_array_equal(of.scaled_mm(a, eye, 2.0, 3.0), t[a] * 6.0)
