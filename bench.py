@@ -19,7 +19,14 @@ headline workloads -- per-head RMSNorm + RoPE of the 1024px Q ([1, 4352, 24,
 128] bf16) and the slab store of the 768px edit prefix ([1, 2560, 24, 128] K
 and V, V to fp8) -- device time per call of prebuilt C-ABI launches back to back (``us``), the
 time per call through the Python API (``api_us``), priced in algorithmic HBM
-bytes against 8 TB/s, beside the same torch computation on the host CPU.
+bytes against 8 TB/s, beside the same torch computation on the host CPU; and
+the W8A8 fp8 linear (FP8Linear, the DiT's projections) at the reference test's
+shape ([1536, 4096] x [4096, 4096]) and at the 1024px layer's fused QKV and
+MLP-out shapes (4352 tokens, H*D = 3072): GEMM device time, TFLOP/s against
+the 5.0 PF dense fp8 peak, the activation quantiser's time, the whole
+FP8Linear call through the Python API, torch._scaled_mm (hipBLASLt, the call
+the reference makes) on the same device for context, and an fp32 matmul of the
+dequantised operands on the host CPU for the reference shape.
 """
 
 from __future__ import annotations
@@ -38,6 +45,7 @@ if ROOT not in sys.path:
 METRIC = "block-causal attn TFLOP/s (unmasked) & % bf16 MFMA peak, 1024px + edit"
 PEAK_BF16_TFLOPS = 2516.6   # MI355X dense bf16 MFMA: 256 CU x 4096 FLOP/clk x 2.4 GHz ("2.5 PF")
 PEAK_HBM_GBS = 8000.0
+PEAK_FP8_TFLOPS = 5000.0    # MI355X dense fp8 MFMA ("5.0 PF" dense)
 
 
 def parse():
@@ -410,6 +418,62 @@ def side_ops(qik, wls, dev, with_cpu: bool) -> dict:
         ccache = qik.ContiguousKVCache(1, B, P + 272, H, D, v_fp8=True, device="cpu")
         entry["cpu_torch_us"] = round(_cpu_us(lambda: ccache.get_layer(0).store(kc, vc), 3), 1)
     out["slab_store_edit_768_prefix"] = entry
+    out.update(fp8_linear_ops(qik, dev, with_cpu))
+    return out
+
+
+def fp8_linear_ops(qik, dev, with_cpu: bool) -> dict:
+    """The fp8 GEMM (qik_fp8_gemm) at three projection shapes, with its quantiser."""
+    import ctypes
+
+    import torch
+
+    from qwen_image_kernel_amd import _lib
+    from qwen_image_kernel_amd import fp8 as f8
+
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    out = {}
+    shapes = [("fp8_linear_1536x4096x4096", 1536, 4096, 4096, "reference test shape (tests/test_fp8.py:16)"),
+              ("fp8_linear_4352x9216x3072", 4352, 9216, 3072, "1024px layer, fused QKV (H*D = 3072)"),
+              ("fp8_linear_4352x3072x12288", 4352, 3072, 12288, "1024px layer, MLP out (hidden 4*3072)")]
+    g = torch.Generator(device="cuda").manual_seed(78)
+    for name, M, N, K, what in shapes:
+        x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+        lin = torch.nn.Linear(K, N, bias=False, dtype=torch.bfloat16, device=dev)
+        with torch.no_grad():
+            lin.weight.normal_(0.0, 0.02, generator=g)
+        fq = f8.FP8Linear.from_linear(lin)
+        xq, sa = f8.quantize_tensorwise(x)
+        y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+        a = f8._gemm_args(xq, fq.weight, sa, fq.weight_scale, None, y)
+        us = _batch_us(lambda: lib.qik_fp8_gemm(ctypes.byref(a), stream), 30)
+        qa = f8.quant_args(x.reshape(-1), xq, sa, _lib.FP8_ACTIVATION)
+        nws = ctypes.c_int64()
+        _lib.check(lib.qik_fp8_quant_workspace_size(ctypes.byref(qa), ctypes.byref(nws)), "workspace size")
+        qws = torch.empty(max(nws.value, 4), dtype=torch.uint8, device=dev)
+        q_us = _batch_us(lambda: lib.qik_fp8_quantize(ctypes.byref(qa), qws.data_ptr(), nws.value, stream), 30)
+        api_us = _event_us(lambda: fq(x), 20)
+        flops = 2.0 * M * N * K
+        entry = {"shape_mnk": [M, N, K], "what": what, "kernel": "fp8_gemm_kernel (qik_fp8_gemm)",
+                 "us": round(us, 2), "tflops": round(flops / (us * 1e-6) / 1e12, 1),
+                 "frac_fp8_peak": round(flops / (us * 1e-6) / 1e12 / PEAK_FP8_TFLOPS, 4),
+                 "quantize_us": round(q_us, 2),
+                 "quantize_gbs": round(M * K * 3 / (q_us * 1e-6) / 1e9, 1), "api_us": round(api_us, 2)}
+        try:
+            wt = fq.weight.t()
+            sm_us = _batch_us(lambda: torch._scaled_mm(xq, wt, scale_a=sa, scale_b=fq.weight_scale,
+                                                       out_dtype=torch.bfloat16), 30)
+            entry["torch_scaled_mm_us"] = round(sm_us, 2)
+        except (RuntimeError, NotImplementedError) as e:
+            entry["torch_scaled_mm_us"] = f"unavailable: {type(e).__name__}"
+        if with_cpu and M == 1536:
+            xd = (xq.float() * sa).cpu()
+            wd = (fq.weight.float() * fq.weight_scale).cpu()
+            entry["cpu_fp32_matmul_us"] = round(_cpu_us(lambda: xd @ wd.t(), 2), 1)
+            entry["cpu_threads"] = torch.get_num_threads()
+        out[name] = entry
+        del x, lin, fq, xq, y
     return out
 
 

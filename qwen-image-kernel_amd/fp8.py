@@ -68,6 +68,19 @@ def _quant_workspace(dev: torch.device, stream: int, nbytes: int) -> torch.Tenso
     return ws
 
 
+def quant_args(flat: torch.Tensor, out: torch.Tensor, scale: torch.Tensor, mode: int) -> _lib.QikFp8QuantArgs:
+    """The qik_fp8_quantize argument struct for a contiguous device tensor (no device work)."""
+    a = _lib.QikFp8QuantArgs()
+    a.abi_version = _lib.ABI_VERSION
+    a.dtype = _IN_DTYPES[flat.dtype]
+    a.mode = mode
+    a.x = flat.data_ptr()
+    a.out = out.data_ptr()
+    a.scale = scale.data_ptr()
+    a.n = flat.numel()
+    return a
+
+
 def _quantize(x: torch.Tensor, mode: int) -> tuple[torch.Tensor, torch.Tensor]:
     """codes (x's shape, fp8e4m3fn) and scale ([1] fp32) of a device tensor."""
     if not x.is_cuda:
@@ -82,14 +95,7 @@ def _quantize(x: torch.Tensor, mode: int) -> tuple[torch.Tensor, torch.Tensor]:
     dev = x.device
     out = torch.empty(flat.shape, dtype=torch.float8_e4m3fn, device=dev)
     scale = torch.empty(1, dtype=torch.float32, device=dev)
-    a = _lib.QikFp8QuantArgs()
-    a.abi_version = _lib.ABI_VERSION
-    a.dtype = _IN_DTYPES[x.dtype]
-    a.mode = mode
-    a.x = flat.data_ptr()
-    a.out = out.data_ptr()
-    a.scale = scale.data_ptr()
-    a.n = flat.numel()
+    a = quant_args(flat, out, scale, mode)
     lib = _lib.load()
     with torch.cuda.device(dev):
         need = ctypes.c_int64(0)
