@@ -167,10 +167,18 @@ int qik_attn_fwd_noalloc(const qik_attn_args* args, void* stream);
  * loc * 8 + x): its row block (-1: no work), its piece and its workspace
  * group (-1: not split).  The second piece of a row block with fewer than 16
  * KV tiles is skipped on the device (the first runs the whole row block).
- * `split` = 0 gives qik_attn_fwd's assignment. */
+ * `split` = 0 gives qik_attn_fwd's assignment.  This form assumes the 8 XCDs
+ * of an MI355X; the launches use the XCD count the device reports. */
 int qik_attn_work_map(int64_t n_items, int32_t n_row_blocks, int32_t slots_per_xcd, int32_t split,
                       int32_t* item, int32_t* piece, int32_t* group, int64_t cap, int64_t* grid,
                       int64_t* ngroups, int32_t* pieces);
+
+/* The same for a device whose workgroups are dealt to n_xcds XCDs (1..32):
+ * queue position loc of XCD x at index loc * n_xcds + x.  No counterpart in
+ * the reference (host-side check of the launch plan). */
+int qik_attn_work_map_xcds(int64_t n_items, int32_t n_row_blocks, int32_t slots_per_xcd, int32_t split,
+                           int32_t n_xcds, int32_t* item, int32_t* piece, int32_t* group, int64_t cap,
+                           int64_t* grid, int64_t* ngroups, int32_t* pieces);
 
 /* Host mirror of the KV-tile schedule the kernel runs: for each row block m
  * of BM rows, the number of KV tiles visited, summed over the slab and fresh

@@ -203,6 +203,13 @@ EXPORTS = (
          ctypes.POINTER(ctypes.c_int32)),
     ),
     (
+        "qik_attn_work_map_xcds",
+        ctypes.c_int,
+        (ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p,
+         ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.POINTER(ctypes.c_int64),
+         ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int32)),
+    ),
+    (
         "qik_attn_tile_schedule",
         ctypes.c_int,
         (ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p),

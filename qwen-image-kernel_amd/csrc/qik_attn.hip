@@ -80,8 +80,8 @@ struct Params {
   char* ws_slots;                  // split items: plan.ns partial-state slots per group
   unsigned* ctl;                   // NULL: one workgroup per unit; else the control words
                                    // (QIK_ATTN_WS_CTL_BYTES, zero between launches):
-                                   // [0, NXCD) queue heads, [NXCD, 2 NXCD) exits,
-                                   // [2 NXCD, ...) arrivals per group
+                                   // [0, nx) queue heads, [NXCD_MAX, NXCD_MAX + nx)
+                                   // exits, [2 NXCD_MAX, ...) arrivals per group
   int64_t sq[3], skn[3], svn[3], skc[3], svc[3], so[3];  // b, s, h strides in elements
   int64_t svalid_b;
   int SQ, SN, P, H, KV;
@@ -307,15 +307,16 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params args
   // positions come from the counter, drawn at the end of a unit's tile loop so
   // that the atomic's round trip overlaps the unit's merge and store.
   const bool pulled = args.ctl != nullptr;
-  const int xcd = (int)(blockIdx.x % NXCD);
-  const int gx = (int)(gridDim.x / NXCD);
+  const int nx = args.plan.nx;
+  const int xcd = (int)(blockIdx.x % nx);
+  const int gx = (int)(gridDim.x / nx);
   int pend = -1;  // thread 0: the position drawn at the end of the last tile loop
   for (int first = 1;; first = 0) {
     int bidv = (int)blockIdx.x;
     if (pulled) {
       if (tid == 0) {
         snext = pend >= 0 ? pend
-              : first ? (int)(blockIdx.x / NXCD)
+              : first ? (int)(blockIdx.x / nx)
                       : gx + (int)__hip_atomic_fetch_add(args.ctl + xcd, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
       pend = -1;
@@ -323,7 +324,7 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params args
       const int loc = snext;
       __syncthreads();  // every thread has read snext before the next unit's head rewrites it
       if (loc >= args.plan.wpx) break;
-      bidv = loc * NXCD + xcd;
+      bidv = loc * nx + xcd;
     } else if (!first) {
       break;
     }
@@ -647,14 +648,20 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params args
     // ---- split item: both pieces publish their partial state; the second to
     // arrive combines the two in piece order (so the result does not depend
     // on which piece that is) and writes the output.  Nothing waits on another
-    // workgroup.  The slots are written with device-scope (sc1, write-through)
-    // stores that complete before the arrival count moves, instead of an
-    // agent-scope fence, which would write back and invalidate the whole L2
-    // that the K/V tiles of the other workgroups live in.  The second piece reads
-    // the other's with plain loads: a slot line is read once per launch, after it was
-    // written, and caches start a launch invalidated, so no cache on the way
-    // can hold an older copy; the pieces of an item come from one XCD's queue,
-    // so the lines are normally still in that XCD's L2.
+    // workgroup.  Ordering, at agent (device) scope:
+    //   * each piece writes its slot with device-scope stores (sc1: written
+    //     through past the XCD's L2), then waits for all of them to complete
+    //     (vmcnt(0)) before its barrier and its arrival atomic, so the slot
+    //     is visible device-wide before the arrival count moves (a release
+    //     made of the completion wait; the atomic itself is agent-scope);
+    //   * the piece that sees the count at 1 reads the other slot with
+    //     device-scope loads (sc1: served from the coherence point, not from a
+    //     CU or XCD cache), issued only after its atomic returned (barrier in
+    //     between), so they observe those stores whichever CU or XCD either
+    //     piece ran on.
+    // There is no agent-scope fence: on gfx950 one is an L2 writeback plus an
+    // L2 invalidate of the whole XCD, which throws away the other workgroups'
+    // K/V lines (measured: the first version was 30% slower with it).
     const Params pe = reread_args();
     if (pulled && tid == 0) pend = gx + (int)__hip_atomic_fetch_add(pe.ctl + xcd, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     float l_part = l_run;
@@ -678,7 +685,7 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params args
       __syncthreads();
       if (tid == 0) {
         // arrival count of the group, 0 between launches: the last piece puts it back
-        unsigned* const word = pe.ctl + 2 * NXCD + wk.group;
+        unsigned* const word = pe.ctl + 2 * NXCD_MAX + wk.group;
         const unsigned before = __hip_atomic_fetch_add(word, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const bool last = before == 1u;
         if (last) __hip_atomic_store(word, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -691,7 +698,7 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params args
       // arithmetic whichever of them arrived last
       const auto other = make_rsrc(gslots + (wk.piece ^ 1) * SB, SB);
       const f32x2 mlo = __builtin_bit_cast(
-          f32x2, __builtin_amdgcn_raw_buffer_load_b64(other, (uint32_t)(OB + tid * 8), 0, 0));
+          f32x2, __builtin_amdgcn_raw_buffer_load_b64(other, (uint32_t)(OB + tid * 8), 0, SC1));
       const bool p1 = wk.piece != 0;
       const float m0 = p1 ? mlo[0] : m_run, m1 = p1 ? m_run : mlo[0];
       const float l0 = p1 ? mlo[1] : l_run, l1 = p1 ? l_run : mlo[1];
@@ -704,7 +711,7 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params args
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4) {
           const f32x4 v = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                        other, (uint32_t)(((db * 4 + q4) * NTHREADS + tid) * 16), 0, 0));
+                                                        other, (uint32_t)(((db * 4 + q4) * NTHREADS + tid) * 16), 0, SC1));
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const float o0 = p1 ? v[e] : oacc[db][4 * q4 + e];
@@ -735,11 +742,11 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params args
   // ---- the last workgroup of the XCD to leave puts its queue words back to 0
   // (every workgroup of the XCD has drawn its last position by then)
   if (pulled && tid == 0) {
-    const unsigned g = gridDim.x / NXCD;
-    const unsigned before = __hip_atomic_fetch_add(args.ctl + NXCD + xcd, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned g = gridDim.x / nx;
+    const unsigned before = __hip_atomic_fetch_add(args.ctl + NXCD_MAX + xcd, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (before == g - 1) {
       __hip_atomic_store(args.ctl + xcd, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(args.ctl + NXCD + xcd, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(args.ctl + NXCD_MAX + xcd, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }
@@ -817,9 +824,26 @@ int schedule_one(int64_t Lmax, int64_t P, int64_t SN, bool has_cache) {
 }
 
 // Workgroups one XCD of the current device holds at once for kernel `which`
-// (0..11, see pick_index): occupancy per CU x CUs / NXCD, cached per device.
+// (0..11, see pick_index): occupancy per CU x CUs / XCDs, cached per device.
 constexpr int MAX_DEVICES = 64;
 std::atomic<int> g_slots[MAX_DEVICES][12];
+std::atomic<int> g_xcds[MAX_DEVICES];
+
+// XCDs of the current device (hipDeviceAttributeNumberOfXccs; NXCD if the
+// runtime cannot say), clamped to [1, NXCD_MAX], cached per device.
+int device_xcds() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return NXCD;
+  if (dev >= 0 && dev < MAX_DEVICES) {
+    const int c = g_xcds[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
+  int nx = 0;
+  if (hipDeviceGetAttribute(&nx, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess || nx <= 0) nx = NXCD;
+  nx = std::min(std::max(nx, 1), NXCD_MAX);
+  if (dev >= 0 && dev < MAX_DEVICES) g_xcds[dev].store(nx, std::memory_order_relaxed);
+  return nx;
+}
 
 int pick_index(int D, bool fp16, bool vfp8, bool kv) {
   return 2 * ((D == 128 ? 3 : 0) + (fp16 ? 1 : (vfp8 ? 2 : 0))) + (kv ? 1 : 0);
@@ -842,7 +866,7 @@ int slots_per_xcd(kernel_fn fn, int which, int* out) {
           hipSuccess ||
       occ <= 0)
     return QIK_ERR_DEVICE;
-  const int sx = std::max(1, occ * cus / NXCD);
+  const int sx = std::max(1, occ * cus / device_xcds());
   if (dev >= 0 && dev < MAX_DEVICES) g_slots[dev][which].store(sx, std::memory_order_relaxed);
   *out = sx;
   return QIK_OK;
@@ -875,24 +899,25 @@ int plan_launch(const qik_attn_args* a, bool split, Launch* L) {
   L->grid = 0;
   memset(&L->plan, 0, sizeof(L->plan));
   if (n == 0) return QIK_OK;
+  const int nx = device_xcds();
   int sx = 1;
   if (split) {
     const int st = slots_per_xcd(L->fn, pick_index((int)a->D, fp16, vfp8, kv), &sx);
     if (st != QIK_OK) return st;
-    L->plan = make_plan((int)n, (int)nmb, sx, 1, (a->flags & QIK_UNIFORM_L) ? 0 : 1);
-    // queue positions are mapped through loc * NXCD + x, which must fit an
+    L->plan = make_plan((int)n, (int)nmb, sx, 1, (a->flags & QIK_UNIFORM_L) ? 0 : 1, nx);
+    // queue positions are mapped through loc * nx + x, which must fit an
     // int, and the arrival words must fit the fixed control region (the same
     // for every shape, so that no launch leaves slot data where another
     // launch keeps its control words)
-    if ((int64_t)NXCD * L->plan.wpx <= INT_MAX && 2 * NXCD + L->plan.ngroups <= QIK_ATTN_WS_CTL_BYTES / 4) {
-      L->grid = (int64_t)NXCD * std::min(sx, L->plan.wpx);
+    if ((int64_t)nx * L->plan.wpx <= INT_MAX && 2 * NXCD_MAX + L->plan.ngroups <= QIK_ATTN_WS_CTL_BYTES / 4) {
+      L->grid = (int64_t)nx * std::min(sx, L->plan.wpx);
       L->ctl_bytes = QIK_ATTN_WS_CTL_BYTES;
       L->ws_bytes = L->ctl_bytes + (int64_t)L->plan.ngroups * L->plan.ns * L->slot;
       return QIK_OK;
     }
   }
-  L->plan = make_plan((int)n, (int)nmb, sx, 0);
-  L->grid = (int64_t)NXCD * L->plan.wpx;
+  L->plan = make_plan((int)n, (int)nmb, sx, 0, 1, nx);
+  L->grid = (int64_t)nx * L->plan.wpx;
   return QIK_OK;
 }
 
@@ -1095,10 +1120,19 @@ int qik_attn_fwd_noalloc(const qik_attn_args* a, void* stream) {
 int qik_attn_work_map(int64_t n_items, int32_t n_row_blocks, int32_t slots_per_xcd, int32_t split,
                       int32_t* item, int32_t* piece, int32_t* group, int64_t cap, int64_t* grid,
                       int64_t* ngroups, int32_t* pieces) {
+  return qik_attn_work_map_xcds(n_items, n_row_blocks, slots_per_xcd, split, qik::NXCD, item, piece, group, cap,
+                                grid, ngroups, pieces);
+}
+
+int qik_attn_work_map_xcds(int64_t n_items, int32_t n_row_blocks, int32_t slots_per_xcd, int32_t split,
+                           int32_t n_xcds, int32_t* item, int32_t* piece, int32_t* group, int64_t cap,
+                           int64_t* grid, int64_t* ngroups, int32_t* pieces) {
   if (grid == nullptr || ngroups == nullptr) return QIK_ERR_NULL_ARG;
   if (n_items < 0 || n_items > INT_MAX || n_row_blocks < 1 || slots_per_xcd < 1) return QIK_ERR_SHAPE;
-  const qik::WorkPlan pl = qik::make_plan((int)n_items, n_row_blocks, slots_per_xcd, split ? 1 : 0);
-  *grid = (int64_t)qik::NXCD * pl.wpx;
+  if (n_xcds < 1 || n_xcds > qik::NXCD_MAX) return QIK_ERR_SHAPE;
+  const qik::WorkPlan pl = qik::make_plan((int)n_items, n_row_blocks, slots_per_xcd, split ? 1 : 0, 1, n_xcds);
+  if ((int64_t)pl.nx * pl.wpx > INT_MAX) return QIK_ERR_SHAPE;
+  *grid = (int64_t)pl.nx * pl.wpx;
   *ngroups = pl.ngroups;
   if (pieces != nullptr) *pieces = pl.ns;
   if (item == nullptr && piece == nullptr && group == nullptr) return QIK_OK;

@@ -3,9 +3,13 @@
 //
 // A work item is one row block (BM query rows of one (b, h)), numbered
 // (b, h)-major with the heaviest row block of a head first.  Workgroups are
-// dealt to the 8 XCDs round-robin (XCD = blockIdx % 8), so XCD x runs the
-// workgroups x, x+8, ...; each XCD gets a contiguous run of items (per + 1 on
-// the first `rem` XCDs, per on the rest) so that a head's K/V stays in one L2.
+// dealt to the device's nx XCDs round-robin (XCD = blockIdx % nx; nx = 8 on
+// MI355X, the hardware's dealing order measured there), so XCD x runs the
+// workgroups x, x+nx, ...; each XCD gets a contiguous run of items (per + 1
+// on the first `rem` XCDs, per on the rest) so that a head's K/V stays in one
+// L2.  Coverage does not depend on that dealing order: the plan hands every
+// item to exactly one queue position whatever nx is, so a device that deals
+// workgroups differently (or reports another XCD count) only loses locality.
 //
 // An XCD holds `sx` workgroups at once.  Items that fill whole rounds of sx
 // run as one unit each; each item of the last, partly filled round is split
@@ -24,8 +28,8 @@
 // biggest: then the pieces are equal halves.  The two pieces of an item combine
 // their partial softmax states through the workspace slots of its group.
 //
-// plan_work(pl, loc * NXCD + x) is the unit at queue position loc of XCD x;
-// without a workspace the same function maps workgroup bid = loc * NXCD + x.
+// plan_work(pl, loc * nx + x) is the unit at queue position loc of XCD x;
+// without a workspace the same function maps workgroup bid = loc * nx + x.
 
 #pragma once
 
@@ -39,17 +43,19 @@
 
 namespace qik {
 
-constexpr int NXCD = 8;
+constexpr int NXCD = 8;        // XCDs of an MI355X (the plan's default)
+constexpr int NXCD_MAX = 32;   // largest XCD count a plan takes (control-word layout)
 constexpr int MAX_PIECES = 2;
 
 struct WorkPlan {
+  int nx;                // XCDs the workgroups are dealt to (1 .. NXCD_MAX)
   int nmb;               // row blocks per (b, h)
   int per, rem;          // items per XCD: per + 1 on XCDs x < rem, per on the others
   int full_lo, full_hi;  // items an XCD runs whole when it has per / per + 1 items
   int ns;                // pieces per split item (1: nothing is split)
   int wpx;               // positions per XCD: the workgroups of a launch without a
-                         // workspace (grid NXCD * wpx), or the queue length of one
-                         // with (grid NXCD * min(sx, wpx))
+                         // workspace (grid nx * wpx), or the queue length of one
+                         // with (grid nx * min(sx, wpx))
   int mb_major;          // 1: an XCD's items are whole heads, walked rank-major
   int ngroups;           // split items (workspace slot groups of ns slots)
   int even;              // 1: the two pieces are equal halves, else 7/10 and 3/10
@@ -72,11 +78,14 @@ inline int plan_pieces(int r) { return r > 0 ? MAX_PIECES : 1; }
 // holds whole heads walks them rank-major (every head's heaviest row block
 // first, the light ones last, where the split tail is); with equal items it
 // keeps them head-major, which holds fewer heads' K/V in its L2 at once.
-inline WorkPlan make_plan(int n, int nmb, int sx, int split, int ragged = 1) {
+inline WorkPlan make_plan(int n, int nmb, int sx, int split, int ragged = 1, int nx = NXCD) {
   WorkPlan pl;
+  if (nx < 1) nx = 1;
+  if (nx > NXCD_MAX) nx = NXCD_MAX;
+  pl.nx = nx;
   pl.nmb = nmb;
-  pl.per = n / NXCD;
-  pl.rem = n % NXCD;
+  pl.per = n / nx;
+  pl.rem = n % nx;
   if (sx < 1) sx = 1;
   if (split) {
     pl.full_lo = plan_full(pl.per, sx);
@@ -91,14 +100,14 @@ inline WorkPlan make_plan(int n, int nmb, int sx, int split, int ragged = 1) {
   const int w_lo = pl.full_lo + pl.ns * r_lo;
   const int w_hi = pl.rem > 0 ? pl.full_hi + pl.ns * r_hi : 0;
   pl.wpx = w_lo > w_hi ? w_lo : w_hi;
-  pl.ngroups = pl.rem * r_hi + (NXCD - pl.rem) * r_lo;
+  pl.ngroups = pl.rem * r_hi + (nx - pl.rem) * r_lo;
   pl.even = (pl.ns > 1 && pl.full_lo == 0 && pl.full_hi == 0 && pl.wpx <= sx) ? 1 : 0;
   pl.mb_major = (split && ragged && pl.rem == 0 && nmb > 0 && pl.per % nmb == 0) ? 1 : 0;
   return pl;
 }
 
 QIK_HD inline Work plan_work(const WorkPlan& pl, int bid) {
-  const int x = bid % NXCD, loc = bid / NXCD;
+  const int x = bid % pl.nx, loc = bid / pl.nx;
   const int big = x < pl.rem ? 1 : 0;
   const int q = pl.per + big;
   const int full = big ? pl.full_hi : pl.full_lo;

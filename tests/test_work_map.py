@@ -164,3 +164,55 @@ def test_work_map_rejects_bad_arguments():
     # a buffer shorter than the grid
     assert lib.qik_attn_work_map(100, 5, 64, 1, buf.ctypes.data, buf.ctypes.data, buf.ctypes.data, 4,
                                  ctypes.byref(g), ctypes.byref(p), None) == -5
+
+
+def work_map_xcds(n, nmb, sx, split, nx):
+    lib = _lib.load()
+    grid, ngroups, ns = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int32()
+    assert lib.qik_attn_work_map_xcds(n, nmb, sx, split, nx, None, None, None, 0, ctypes.byref(grid),
+                                      ctypes.byref(ngroups), ctypes.byref(ns)) == 0
+    g = grid.value
+    item, piece, group = (np.full(max(g, 1), -7, dtype=np.int32) for _ in range(3))
+    assert lib.qik_attn_work_map_xcds(n, nmb, sx, split, nx, item.ctypes.data, piece.ctypes.data,
+                                      group.ctypes.data, g, ctypes.byref(grid), ctypes.byref(ngroups), None) == 0
+    return item[:g], piece[:g], group[:g], ngroups.value, ns.value
+
+
+@pytest.mark.parametrize("nx", [1, 2, 3, 4, 6, 8, 16, 32])
+@pytest.mark.parametrize("n,nmb,sx", [(816, 34, 64), (768, 32, 64), (216, 9, 64), (12, 3, 64), (850, 34, 30),
+                                      (2784, 58, 16)])
+@pytest.mark.parametrize("split", [0, 1])
+def test_plan_for_another_xcd_count_runs_every_row_block_once(n, nmb, sx, split, nx):
+    """A device that reports another XCD count (a partitioned MI355X shows 1,
+    2 or 4) gets a plan over that many queues: still every row block whole
+    exactly once or as both pieces of one group, groups dense, the grid a
+    multiple of the XCD count."""
+    item, piece, group, ngroups, ns = work_map_xcds(n, nmb, sx, split, nx)
+    assert len(item) % nx == 0
+    whole = np.zeros(n, dtype=np.int64)
+    pieces = {}
+    for it, pc, gr in zip(item, piece, group):
+        if it < 0:
+            continue
+        if gr < 0:
+            whole[it] += 1
+        else:
+            assert 0 <= gr < ngroups
+            pieces.setdefault(it, []).append((pc, gr))
+    for it, ps in pieces.items():
+        assert sorted(pc for pc, _ in ps) == list(range(ns)) and len({gr for _, gr in ps}) == 1
+        assert whole[it] == 0
+    assert sorted({gr for ps in pieces.values() for _, gr in ps}) == list(range(ngroups))
+    covered = whole + np.array([1 if i in pieces else 0 for i in range(n)])
+    assert (covered == 1).all()
+    if nx == NXCD:
+        same = work_map(n, nmb, sx, split)
+        np.testing.assert_array_equal(same[0], item)
+
+
+def test_work_map_xcds_rejects_bad_counts():
+    lib = _lib.load()
+    grid, ngroups = ctypes.c_int64(), ctypes.c_int64()
+    for nx in (0, -1, 33):
+        assert lib.qik_attn_work_map_xcds(100, 10, 8, 1, nx, None, None, None, 0, ctypes.byref(grid),
+                                          ctypes.byref(ngroups), None) == -5
