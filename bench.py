@@ -102,7 +102,7 @@ def all_workloads() -> None:
     torch.cuda.set_device(dev)
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     res, runs = {}, []
-    for name in ("t2i_512", "t2i_1024", "edit_768", "multiref_cfg"):
+    for name in ("t2i_512", "t2i_1024", "edit_768", "multiref_cfg", "ref_decode_1024"):
         wl = wls.workload(name)
         nl = 4 if name == "multiref_cfg" else 8
         layers = [wls.make_inputs(wl, seed=40 + i, device="cuda", gen_device="cuda") for i in range(nl)]
@@ -418,6 +418,23 @@ def side_ops(qik, wls, dev, with_cpu: bool) -> dict:
         ccache = qik.ContiguousKVCache(1, B, P + 272, H, D, v_fp8=True, device="cpu")
         entry["cpu_torch_us"] = round(_cpu_us(lambda: ccache.get_layer(0).store(kc, vc), 3), 1)
     out["slab_store_edit_768_prefix"] = entry
+
+    # one attention call at the smallest benchmark shape, where host time shows
+    from qwen_image_kernel_amd.attention import make_args
+
+    sm = wls.workload("t2i_512")
+    inp = wls.make_inputs(sm, seed=79, device=dev, gen_device="cuda")
+    o = torch.empty_like(inp["query"])
+    aa = make_args(inp["query"], inp["key"], inp["value"], inp["prefix_lengths"], None, o, None, None, None, False)
+    nws = ctypes.c_int64()
+    _lib.check(lib.qik_attn_workspace_size(ctypes.byref(aa), ctypes.byref(nws)), "workspace size")
+    aws = torch.zeros(max(nws.value, 256), dtype=torch.uint8, device=dev)
+    us = _batch_us(lambda: lib.qik_attn_fwd_ws(ctypes.byref(aa), aws.data_ptr(), nws.value, stream), 50)
+    api_us = _event_us(lambda: qik.block_causal_flash_attention(inp["query"], inp["key"], inp["value"],
+                                                                inp["prefix_lengths"], None), 20)
+    out["attention_t2i_512_call"] = {"shape": [sm.B, sm.SQ, sm.H, sm.D], "kernel": "attn_fwd_kernel (qik_attn_fwd_ws)",
+                                     "us": round(us, 2), "api_us": round(api_us, 2),
+                                     "tflops": round(sm.flops() / us / 1e6, 1)}
     out.update(fp8_linear_ops(qik, dev, with_cpu))
     return out
 

@@ -9,6 +9,9 @@ Five shapes, from the CPU-checkable tiny case up to the multi-reference edit:
                    256 text + 2304 condition tokens (48x48; bf16 K, fp8 V) + 4096 fresh keys
 * ``multiref_cfg`` B2 H24 (cond/uncond), 256 text + 3 x 1024 condition blocks in the slab
                    + 4096 fresh target tokens, all 7424 rows queried, ragged L
+* ``ref_decode_1024`` B1 H32, the shape of the reference's one published kernel number
+                   (RESULTS.md:27, tools/sweep_attention2.py:95): 4096 target queries against
+                   a 256-token text slab (bf16 K and V) + 4096 fresh keys, uniform L
 
 Inputs are N(0, 1) in fp32 from a seeded ``torch.Generator`` cast to bf16; the
 slab V is quantised to fp8 per (b, h) by ``ContiguousKVCache.store``.  The
@@ -100,6 +103,8 @@ def workload(name: str) -> Workload:
     if name == "multiref_cfg":
         segs, p = _layout([("text", 256), ("img", 1024), ("img", 1024), ("img", 1024)])
         return Workload(name, 2, 24, 128, p + 4096, p, 4096, segs, p, False, True)
+    if name == "ref_decode_1024":
+        return Workload(name, 1, 32, 128, 4096, 256, 4096, [], 0, True, False)
     raise KeyError(f"unknown workload {name!r}")
 
 
