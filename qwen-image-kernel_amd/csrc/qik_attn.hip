@@ -649,16 +649,18 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params args
     // arrive combines the two in piece order (so the result does not depend
     // on which piece that is) and writes the output.  Nothing waits on another
     // workgroup.  Ordering, at agent (device) scope:
-    //   * each piece writes its slot with device-scope stores (sc1: written
+    //   * a piece that publishes writes its slot with device-scope stores (sc1: written
     //     through past the XCD's L2), then waits for all of them to complete
     //     (vmcnt(0)) before its barrier and its arrival atomic, so the slot
     //     is visible device-wide before the arrival count moves (a release
     //     made of the completion wait; the atomic itself is agent-scope);
-    //   * the piece that sees the count at 1 reads the other slot with
+    //   * the piece that sees the count at 1 (before publishing, or as the
+    //     value its own increment returned) reads the other slot with
     //     device-scope loads (sc1: served from the coherence point, not from a
-    //     CU or XCD cache), issued only after its atomic returned (barrier in
+    //     CU or XCD cache), issued only after that atomic returned (barrier in
     //     between), so they observe those stores whichever CU or XCD either
-    //     piece ran on.
+    //     piece ran on.  Both pieces may publish (each sees 0 first); then the
+    //     second increment merges, as before.
     // There is no agent-scope fence: on gfx950 one is an L2 writeback plus an
     // L2 invalidate of the whole XCD, which throws away the other workgroups'
     // K/V lines (measured: the first version was 30% slower with it).
@@ -670,29 +672,40 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params args
       constexpr int SB = slot_bytes<D>();
       constexpr int SC1 = 16;  // cache policy: device scope
       char* const gslots = pe.ws_slots + (int64_t)wk.group * pe.plan.ns * SB;
-      const auto mine = make_rsrc(gslots + wk.piece * SB, SB);
+      unsigned* const word = pe.ctl + 2 * NXCD_MAX + wk.group;
+      // arrival count of the group (0 between launches: whoever merges puts
+      // it back).  A piece that finds the other one already arrived merges
+      // at once and never writes its own slot; otherwise it publishes its
+      // slot and arrives, and the second to arrive merges.
+      if (tid == 0) sred[0] = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 1u ? 1 : 0;
+      __syncthreads();
+      const bool other_first = sred[0] != 0;
+      __syncthreads();  // every thread has read sred[0] before it is reused
+      if (other_first) {
+        if (tid == 0) __hip_atomic_store(word, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      } else {
+        const auto mine = make_rsrc(gslots + wk.piece * SB, SB);
 #pragma unroll
-      for (int db = 0; db < DBLK; ++db)
+        for (int db = 0; db < DBLK; ++db)
 #pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-          const f32x4 v = {oacc[db][4 * q4 + 0], oacc[db][4 * q4 + 1], oacc[db][4 * q4 + 2], oacc[db][4 * q4 + 3]};
-          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), mine,
-                                                 (uint32_t)(((db * 4 + q4) * NTHREADS + tid) * 16), 0, SC1);
+          for (int q4 = 0; q4 < 4; ++q4) {
+            const f32x4 v = {oacc[db][4 * q4 + 0], oacc[db][4 * q4 + 1], oacc[db][4 * q4 + 2], oacc[db][4 * q4 + 3]};
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), mine,
+                                                   (uint32_t)(((db * 4 + q4) * NTHREADS + tid) * 16), 0, SC1);
+          }
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f32x2{m_run, l_run}), mine,
+                                              (uint32_t)(OB + tid * 8), 0, SC1);
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the slot has reached device scope
+        __syncthreads();
+        if (tid == 0) {
+          const unsigned before = __hip_atomic_fetch_add(word, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          const bool last = before == 1u;
+          if (last) __hip_atomic_store(word, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          sred[0] = last ? 1 : 0;
         }
-      __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f32x2{m_run, l_run}), mine,
-                                            (uint32_t)(OB + tid * 8), 0, SC1);
-      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the slot has reached device scope
-      __syncthreads();
-      if (tid == 0) {
-        // arrival count of the group, 0 between launches: the last piece puts it back
-        unsigned* const word = pe.ctl + 2 * NXCD_MAX + wk.group;
-        const unsigned before = __hip_atomic_fetch_add(word, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const bool last = before == 1u;
-        if (last) __hip_atomic_store(word, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        sred[0] = last ? 1 : 0;
+        __syncthreads();
+        if (sred[0] == 0) continue;  // not the last piece: the last one finishes the item
       }
-      __syncthreads();
-      if (sred[0] == 0) continue;  // not the last piece: the last one finishes the item
 
       // the other piece's state; the two combine in piece order, the same
       // arithmetic whichever of them arrived last
