@@ -18,7 +18,9 @@ the two HBM-bound kernels beside the attention call, each at its shape in the
 headline workloads -- per-head RMSNorm + RoPE of the 1024px Q ([1, 4352, 24,
 128] bf16) and the slab store of the 768px edit prefix ([1, 2560, 24, 128] K
 and V, V to fp8) -- device time per call of prebuilt C-ABI launches back to back (``us``), the
-time per call through the Python API (``api_us``), priced in algorithmic HBM
+time per call of Python API calls issued back to back (``api_us``: two events around the
+batch, so it is the device time unless the host is slower) and the host time per API call
+(``host_us``: wall time of a loop of calls, the device running behind), priced in algorithmic HBM
 bytes against 8 TB/s, beside the same torch computation on the host CPU; and
 the W8A8 fp8 linear (FP8Linear, the DiT's projections) at the reference test's
 shape ([1536, 4096] x [4096, 4096]) and at the 1024px layer's fused QKV and
@@ -310,24 +312,6 @@ def clock_under_load(calls, dev, seconds: float = 1.5) -> dict:
     return out
 
 
-def _event_us(fn, reps: int) -> float:
-    """Average device time of fn() in microseconds (HIP events on the current stream)."""
-    import torch
-
-    for _ in range(3):
-        fn()
-    torch.cuda.synchronize()
-    ts = []
-    for _ in range(reps):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        fn()
-        e1.record()
-        ts.append((e0, e1))
-    torch.cuda.synchronize()
-    return sum(a.elapsed_time(b) for a, b in ts) / reps * 1e3
-
-
 def _batch_us(fn, reps: int) -> float:
     """Device time per call of fn() launched back to back (two events around the batch)."""
     import torch
@@ -342,6 +326,22 @@ def _batch_us(fn, reps: int) -> float:
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / reps * 1e3
+
+
+def _host_us(fn, reps: int) -> float:
+    """Host (wall) time per call of fn() in a loop that only issues work: the
+    device runs behind and is synchronised once, after the loop."""
+    import torch
+
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        fn()
+    t1 = time.perf_counter()
+    torch.cuda.synchronize()
+    return (t1 - t0) / reps * 1e6
 
 
 def _cpu_us(fn, reps: int) -> float:
@@ -375,10 +375,11 @@ def side_ops(qik, wls, dev, with_cpu: bool) -> dict:
     y = torch.empty_like(x)
     ra = fused.rms_rope_args(x, w, cos, sin, y, 1e-6)
     us = _batch_us(lambda: lib.qik_rms_rope(ctypes.byref(ra), stream), 50)
-    api_us = _event_us(lambda: qik.fused_rms_norm_rope(x, w, freqs, 1e-6), 20)
+    api = lambda: qik.fused_rms_norm_rope(x, w, freqs, 1e-6)
+    api_us, host_us = _batch_us(api, 50), _host_us(api, 200)
     nbytes = 2 * B * S * H * D * 2 + D * 4 + S * (D // 2) * 8   # x in, out, weight, cos/sin
     entry = {"shape": [B, S, H, D], "kernel": "rms_rope_kernel<128,bf16>", "us": round(us, 2),
-             "api_us": round(api_us, 2),
+             "api_us": round(api_us, 2), "host_us": round(host_us, 2),
              "algorithmic_bytes": nbytes, "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
              "frac_hbm": round(nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4)}
     if with_cpu:
@@ -405,11 +406,13 @@ def side_ops(qik, wls, dev, with_cpu: bool) -> dict:
     ws = torch.empty(max(nws.value, 4), dtype=torch.uint8, device=dev)
     us = _batch_us(lambda: lib.qik_slab_store_ws(ctypes.byref(sa), ws.data_ptr(), nws.value, stream), 50)
     us3 = _batch_us(lambda: lib.qik_slab_store(ctypes.byref(sa), stream), 50)
-    api_us = _event_us(lambda: layer.store(k, v), 20)
+    api = lambda: layer.store(k, v)
+    api_us, host_us = _batch_us(api, 50), _host_us(api, 200)
     nbytes = B * P * H * D * (2 + 2 + 2 + 1) + B * H * 4   # k, v in; k bf16, v fp8 out; scales
     entry = {"shape": [B, P, H, D],
              "kernels": "slab_copy_scale_kernel<128> + slab_quant_fp8_kernel<128> (qik_slab_store_ws)",
-             "us": round(us, 2), "api_us": round(api_us, 2), "algorithmic_bytes": nbytes,
+             "us": round(us, 2), "api_us": round(api_us, 2), "host_us": round(host_us, 2),
+             "algorithmic_bytes": nbytes,
              "us_three_launch_form": round(us3, 2),
              "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
              "frac_hbm": round(nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4)}
@@ -430,10 +433,11 @@ def side_ops(qik, wls, dev, with_cpu: bool) -> dict:
     _lib.check(lib.qik_attn_workspace_size(ctypes.byref(aa), ctypes.byref(nws)), "workspace size")
     aws = torch.zeros(max(nws.value, 256), dtype=torch.uint8, device=dev)
     us = _batch_us(lambda: lib.qik_attn_fwd_ws(ctypes.byref(aa), aws.data_ptr(), nws.value, stream), 50)
-    api_us = _event_us(lambda: qik.block_causal_flash_attention(inp["query"], inp["key"], inp["value"],
-                                                                inp["prefix_lengths"], None), 20)
+    api = lambda: qik.block_causal_flash_attention(inp["query"], inp["key"], inp["value"], inp["prefix_lengths"], None)
+    api_us, host_us = _batch_us(api, 50), _host_us(api, 200)
     out["attention_t2i_512_call"] = {"shape": [sm.B, sm.SQ, sm.H, sm.D], "kernel": "attn_fwd_kernel (qik_attn_fwd_ws)",
                                      "us": round(us, 2), "api_us": round(api_us, 2),
+                                     "host_us": round(host_us, 2),
                                      "tflops": round(sm.flops() / us / 1e6, 1)}
     out.update(fp8_linear_ops(qik, dev, with_cpu))
     return out
@@ -470,13 +474,14 @@ def fp8_linear_ops(qik, dev, with_cpu: bool) -> dict:
         _lib.check(lib.qik_fp8_quant_workspace_size(ctypes.byref(qa), ctypes.byref(nws)), "workspace size")
         qws = torch.empty(max(nws.value, 4), dtype=torch.uint8, device=dev)
         q_us = _batch_us(lambda: lib.qik_fp8_quantize(ctypes.byref(qa), qws.data_ptr(), nws.value, stream), 30)
-        api_us = _event_us(lambda: fq(x), 20)
+        api_us, host_us = _batch_us(lambda: fq(x), 30), _host_us(lambda: fq(x), 100)
         flops = 2.0 * M * N * K
         entry = {"shape_mnk": [M, N, K], "what": what, "kernel": "fp8_gemm_kernel (qik_fp8_gemm)",
                  "us": round(us, 2), "tflops": round(flops / (us * 1e-6) / 1e12, 1),
                  "frac_fp8_peak": round(flops / (us * 1e-6) / 1e12 / PEAK_FP8_TFLOPS, 4),
                  "quantize_us": round(q_us, 2),
-                 "quantize_gbs": round(M * K * 3 / (q_us * 1e-6) / 1e9, 1), "api_us": round(api_us, 2)}
+                 "quantize_gbs": round(M * K * 3 / (q_us * 1e-6) / 1e9, 1), "api_us": round(api_us, 2),
+                 "host_us": round(host_us, 2)}
         try:
             wt = fq.weight.t()
             sm_us = _batch_us(lambda: torch._scaled_mm(xq, wt, scale_a=sa, scale_b=fq.weight_scale,

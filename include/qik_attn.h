@@ -19,7 +19,7 @@
 extern "C" {
 #endif
 
-#define QIK_ABI_VERSION 1
+#define QIK_ABI_VERSION 2
 
 /* Element types of q / k / v / out. */
 enum qik_dtype {

@@ -75,6 +75,11 @@ typedef struct qik_slab_store_args {
   int64_t stride_v[3];        /* b, p, h of v                                        */
   int64_t stride_k_dst[3];    /* b, h, p of k_dst                                    */
   int64_t stride_v_dst[3];    /* b, h, p of v_dst                                    */
+  int64_t* length_dst;        /* optional: the store's first launch also writes P
+                                 here (the layer's entry of a device length table,
+                                 kv_cache.py:45 sets it after the store); NULL: not
+                                 written.  Nothing is launched, and nothing written,
+                                 when B*H*P is 0.                                   */
 } qik_slab_store_args;
 
 int qik_slab_store(const qik_slab_store_args* args, void* stream);

@@ -21,7 +21,7 @@ import torch  # noqa: F401  (load order: torch's HIP runtime first)
 LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libqik_attn.so")
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DTYPE_BF16 = 0
 DTYPE_FP16 = 1
@@ -140,6 +140,7 @@ class QikSlabStoreArgs(ctypes.Structure):
         ("stride_v", _i64x3),
         ("stride_k_dst", _i64x3),
         ("stride_v_dst", _i64x3),
+        ("length_dst", ctypes.c_void_p),
     ]
 
 

@@ -226,6 +226,7 @@ struct CopyParams {
   int64_t rows;      // B*H*P
   int64_t P, H;
   int row_bytes;     // D * element size
+  int64_t* len_dst;  // NULL, or where the first launch writes P
 };
 
 // One 16-byte chunk g of the copy of tensor `which` (0 = K, 1 = V).
@@ -248,6 +249,7 @@ __global__ void __launch_bounds__(NTHREADS) slab_copy_kernel(const CopyParams p)
   const int which = blockIdx.y;
   const int64_t g = (int64_t)blockIdx.x * NTHREADS + threadIdx.x;
   if (p.zero != nullptr && which == 0 && g < p.nzero) p.zero[g] = 0.0f;
+  if (p.len_dst != nullptr && which == 0 && g == 0) *p.len_dst = p.P;
   copy_chunk(p, which, g);
 }
 
@@ -344,7 +346,9 @@ template <int D>
 __global__ void __launch_bounds__(QTHREADS) slab_copy_scale_kernel(const CopyParams cp, const QuantParams p,
                                                                    const int ncopy) {
   if ((int)blockIdx.x < ncopy) {
-    copy_chunk(cp, 0, (int64_t)blockIdx.x * QTHREADS + threadIdx.x);
+    const int64_t g = (int64_t)blockIdx.x * QTHREADS + threadIdx.x;
+    if (cp.len_dst != nullptr && g == 0) *cp.len_dst = cp.P;
+    copy_chunk(cp, 0, g);
     return;
   }
   const int bx = (int)blockIdx.x - ncopy;
@@ -511,6 +515,7 @@ int validate_store(const qik_slab_store_args* a, int64_t* rows) {
   if (a->k == nullptr || a->v == nullptr || a->k_dst == nullptr || a->v_dst == nullptr) return QIK_ERR_NULL_ARG;
   if (!aligned_to(a->k, 16) || !aligned_to(a->v, 16) || !aligned_to(a->k_dst, 16)) return QIK_ERR_ALIGN;
   if (!aligned_to(a->v_dst, fp8 ? 8 : 16)) return QIK_ERR_ALIGN;
+  if (a->length_dst != nullptr && !aligned_to(a->length_dst, 8)) return QIK_ERR_ALIGN;
   if (!strides_ok(a->stride_k, 8) || !strides_ok(a->stride_v, 8) || !strides_ok(a->stride_k_dst, 8) ||
       !strides_ok(a->stride_v_dst, 8))
     return QIK_ERR_ALIGN;
@@ -542,6 +547,7 @@ int store(const qik_slab_store_args* a, float* partial, hipStream_t s) {
   cp.P = a->P;
   cp.H = a->H;
   cp.row_bytes = (int)(a->D * 2);
+  cp.len_dst = a->length_dst;
   cp.zero = (fp8 && partial == nullptr) ? a->v_scale : nullptr;
   cp.nzero = a->B * a->H;
   const int64_t threads = rows * (a->D * 2 / 16);

@@ -54,6 +54,50 @@ def fused_rms_norm_rope(
     eps: float,
 ) -> torch.Tensor:
     """RMSNorm over D per (b, s, h), then complex RoPE by position s; returns [B, S, H, D]."""
+    # One lookup per call: everything that only depends on the geometry, the
+    # weight and freqs_cis tensors (and their in-place versions) and eps is
+    # checked and prepared once per key -- the argument struct with the
+    # weight and cos/sin pointers filled in, the output shape.  Only x's and
+    # the output's data pointers change between calls.
+    key = (x.shape, x.stride(), x.dtype, x.device, eps,
+           weight.data_ptr(), weight._version, weight.dtype, weight.shape, weight.stride(), weight.device,
+           freqs_cis.data_ptr(), freqs_cis._version, freqs_cis.dtype, freqs_cis.shape, freqs_cis.stride(),
+           freqs_cis.device)
+    ent = _CALLS.get(key)
+    if ent is None:
+        ent = _prepare(x, weight, freqs_cis, eps)
+        if len(_CALLS) >= 64:
+            _CALLS.clear()
+        _CALLS[key] = ent
+    if ent.contig:
+        x = x.contiguous()
+    out = x.new_empty(ent.shape)
+    a = _lib.QikRmsRopeArgs.from_buffer_copy(ent.args)
+    a.x = x.data_ptr()
+    a.out = out.data_ptr()
+    idx = ent.index
+    if idx != torch.cuda.current_device():
+        with torch.cuda.device(idx):
+            _lib.check(ent.fn(ctypes.byref(a), torch._C._cuda_getCurrentRawStream(idx)), "qik_rms_rope")
+    else:
+        _lib.check(ent.fn(ctypes.byref(a), torch._C._cuda_getCurrentRawStream(idx)), "qik_rms_rope")
+    return out
+
+
+class _Call:
+    """What one (geometry, weight, freqs_cis, eps) key needs at call time."""
+
+    __slots__ = ("args", "shape", "contig", "index", "fn", "keep")
+
+
+# Prepared calls by key (see fused_rms_norm_rope).  An entry keeps the weight
+# and freqs_cis tensors it was built from alive, so the data pointers in a
+# key can never be reused by other tensors while the key is cached; their
+# version counters catch in-place updates.
+_CALLS: dict = {}
+
+
+def _prepare(x, weight, freqs_cis, eps) -> _Call:
     if x.dim() != 4:
         raise ValueError(f"x must be [B, S, H, D], got shape {tuple(x.shape)}")
     if x.dtype not in _DTYPES:
@@ -61,46 +105,23 @@ def fused_rms_norm_rope(
     if not x.is_cuda:
         raise ValueError("x must be a device tensor (the kernel runs on the GPU)")
     B, S, H, D = x.shape
-    if D > 1 and x.stride(-1) != 1:
-        x = x.contiguous()
     if tuple(freqs_cis.shape) != (S, D // 2):
         raise ValueError(f"freqs_cis must be [S, D/2] = {(S, D // 2)}, got {tuple(freqs_cis.shape)}")
+    contig = D > 1 and x.stride(-1) != 1
+    xs = x.contiguous() if contig else x
     w = weight
     if w.dtype != torch.float32 or w.device != x.device or not w.is_contiguous():
         w = weight.to(device=x.device, dtype=torch.float32).contiguous()
     cos, sin = _cos_sin(freqs_cis, x.device)
     out = torch.empty((B, S, H, D), dtype=x.dtype, device=x.device)
-    a = _cached_args(x, w, cos, sin, out, eps)
-    lib = _lib.load()
-    idx = x.device.index
-    if idx != torch.cuda.current_device():
-        with torch.cuda.device(x.device):
-            _lib.check(lib.qik_rms_rope(ctypes.byref(a), torch._C._cuda_getCurrentRawStream(idx)), "qik_rms_rope")
-    else:
-        _lib.check(lib.qik_rms_rope(ctypes.byref(a), torch._C._cuda_getCurrentRawStream(idx)), "qik_rms_rope")
-    return out
-
-
-# Argument structs by geometry (shapes, strides, dtype, eps); only the data
-# pointers change from call to call.  Filling the struct field by field costs
-# more host time than the launch takes on the device.
-_ARGS_CACHE: dict = {}
-
-
-def _cached_args(x, w, cos, sin, out, eps) -> _lib.QikRmsRopeArgs:
-    gkey = (x.device, x.dtype, tuple(x.shape), x.stride(), out.stride(), float(eps))
-    hit = _ARGS_CACHE.get(gkey)
-    if hit is None:
-        if len(_ARGS_CACHE) >= 64:
-            _ARGS_CACHE.clear()
-        hit = _ARGS_CACHE[gkey] = rms_rope_args(x, w, cos, sin, out, eps)
-    a = _lib.QikRmsRopeArgs.from_buffer_copy(hit)
-    a.x = x.data_ptr()
-    a.out = out.data_ptr()
-    a.weight = w.data_ptr()
-    a.cos = cos.data_ptr()
-    a.sin = sin.data_ptr()
-    return a
+    c = _Call()
+    c.args = rms_rope_args(xs, w, cos, sin, out, eps)
+    c.shape = (B, S, H, D)
+    c.contig = contig
+    c.index = x.device.index
+    c.fn = _lib.load().qik_rms_rope
+    c.keep = (weight, w, freqs_cis, cos, sin)
+    return c
 
 
 def rms_rope_args(x, weight, cos, sin, out, eps) -> _lib.QikRmsRopeArgs:

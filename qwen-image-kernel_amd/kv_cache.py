@@ -49,13 +49,17 @@ class _LayerView:
         P = k.shape[1]
         if P > c.capacity:
             raise ValueError(f"prefix of {P} tokens exceeds the slab capacity {c.capacity}")
-        if c.k_buf.is_cuda:
+        if c.k_buf.is_cuda and P > 0 and k.shape[0] > 0 and k.shape[2] > 0:
+            # the store's first launch also writes lengths[layer] = P
             self._store_device(k, v, P)
         else:
-            self._store_torch(k, v, P)
-        # a fill kernel: assigning a Python int to one element is a host-to-device
-        # copy, which a stream under graph capture rejects
-        c.lengths[self._layer:self._layer + 1].fill_(P)
+            if c.k_buf.is_cuda:
+                self._store_device(k, v, P)
+            else:
+                self._store_torch(k, v, P)
+            # a fill kernel: assigning a Python int to one element is a
+            # host-to-device copy, which a stream under graph capture rejects
+            c.lengths[self._layer:self._layer + 1].fill_(P)
         c._host_lengths[self._layer] = P
 
     def _store_device(self, k: torch.Tensor, v: torch.Tensor, P: int) -> None:
@@ -128,6 +132,7 @@ class _LayerView:
         a.stride_v = _lib._i64x3(v.stride(0), v.stride(1), v.stride(2))
         a.stride_k_dst = _lib._i64x3(kd.stride(0), kd.stride(1), kd.stride(2))
         a.stride_v_dst = _lib._i64x3(vd.stride(0), vd.stride(1), vd.stride(2))
+        a.length_dst = c.lengths.data_ptr() + c.lengths.element_size() * self._layer
         return a, (k, v)
 
     def _store_torch(self, k: torch.Tensor, v: torch.Tensor, P: int) -> None:

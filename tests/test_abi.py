@@ -251,6 +251,7 @@ def _store_args(**kw):
     (dict(v_fp8=0), -7),                          # a scale output without fp8 V
     (dict(dtype=_lib.DTYPE_FP16), -7),            # fp8 V only from bf16 (triton_attention.py:159)
     (dict(k=None), -1), (dict(v_dst=0x10004), -8), (dict(stride_k=_lib._i64x3(8192, 260, 128)), -8),
+    (dict(length_dst=0x10004), -8),               # the length is an int64
 ])
 def test_slab_store_rejects_before_any_device_call(kw, code):
     assert _lib.load().qik_slab_store(ctypes.byref(_store_args(**kw)), None) == code
