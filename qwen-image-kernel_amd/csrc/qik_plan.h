@@ -56,7 +56,7 @@ struct WorkPlan {
   int wpx;               // positions per XCD: the workgroups of a launch without a
                          // workspace (grid nx * wpx), or the queue length of one
                          // with (grid nx * min(sx, wpx))
-  int mb_major;          // 1: an XCD's items are whole heads, walked rank-major
+  int mb_major;          // 1: an XCD's items are whole heads, walked rank-major in pairs of heads
   int ngroups;           // split items (workspace slot groups of ns slots)
   int even;              // 1: the two pieces are equal halves, else 7/10 and 3/10
 };
@@ -75,9 +75,12 @@ inline int plan_pieces(int r) { return r > 0 ? MAX_PIECES : 1; }
 
 // n items, nmb per (b, h); `split` = 0 runs every item whole.  `ragged`: the
 // items of a head differ in weight (per-row causal lengths), so an XCD that
-// holds whole heads walks them rank-major (every head's heaviest row block
-// first, the light ones last, where the split tail is); with equal items it
-// keeps them head-major, which holds fewer heads' K/V in its L2 at once.
+// holds whole heads walks them rank-major, two heads at a time (the heaviest
+// row block of both heads first, the light ones last; then the next pair; an
+// odd last head alone, heaviest first), so the split tail holds light row
+// blocks while at most two heads' K/V are in flight in its L2 (measured on
+// MI355X: three heads rank-major fetch 1.4x the bytes at the same time, one
+// head at a time is 8% slower); with equal items it keeps them head-major.
 inline WorkPlan make_plan(int n, int nmb, int sx, int split, int ragged = 1, int nx = NXCD) {
   WorkPlan pl;
   if (nx < 1) nx = 1;
@@ -129,10 +132,14 @@ QIK_HD inline Work plan_work(const WorkPlan& pl, int bid) {
   }
   const int v0 = x * pl.per + (x < pl.rem ? x : pl.rem);
   if (pl.mb_major) {
-    // rank-major over the XCD's heads: the heaviest row block of every head
-    // first, the lightest ones (and so the split tail) last
+    // rank-major over pairs of the XCD's heads, one pair after the other (an
+    // odd last head alone): the heaviest row blocks of a pair first, the
+    // lightest ones of the last pair (or head), and so the split tail, last
     const int heads = q / pl.nmb;
-    w.item = v0 + (k % heads) * pl.nmb + k / heads;
+    const int g = k / (2 * pl.nmb);
+    const int gh = (2 * g + 2 <= heads) ? 2 : 1;
+    const int j = k - g * 2 * pl.nmb;
+    w.item = v0 + (2 * g + j % gh) * pl.nmb + j / gh;
   } else {
     w.item = v0 + k;
   }

@@ -129,17 +129,41 @@ def test_piece_counts_of_the_benchmark_shapes():
     assert work_map(1024, 32, 64, 1)[3:] == (0, 1)
 
 
-def test_rank_major_order_puts_light_row_blocks_last():
-    """24 heads x 34 row blocks: each XCD's run is 3 whole heads, walked heaviest row
-    block of every head first, so the split tail holds the lightest ranks."""
+def test_pair_rank_major_order_puts_light_row_blocks_last():
+    """24 heads x 34 row blocks: each XCD's run is 3 whole heads, walked rank-major over
+    its first two heads (heaviest row block of both first), then the third head
+    heaviest first, so the split tail holds the lightest ranks of the last head and no
+    more than two heads are interleaved anywhere."""
     n, nmb, sx = 816, 34, 64
     item, piece, _, _, _ = work_map(n, nmb, sx, 1)
     for x in range(NXCD):
         mine = item[x::NXCD]
         live = [i for i, pc in zip(mine, piece[x::NXCD]) if i >= 0 and pc == 0]
-        ranks = [i % nmb for i in live]   # item i % nmb == rank (0 = heaviest row block)
-        assert ranks == sorted(ranks)
-        assert len({i // nmb for i in live}) == 3
+        assert len(live) == 3 * nmb and len(set(live)) == 3 * nmb
+        heads = sorted({i // nmb for i in live})
+        assert len(heads) == 3
+        first, last = live[:2 * nmb], live[2 * nmb:]
+        assert {i // nmb for i in first} == set(heads[:2]) and {i // nmb for i in last} == {heads[2]}
+        # item i % nmb == rank (0 = heaviest row block): non-decreasing within each group
+        assert [i % nmb for i in first] == sorted(i % nmb for i in first)
+        assert [i % nmb for i in last] == list(range(nmb))
+        # the two heads of the pair alternate
+        assert all(first[2 * r] // nmb != first[2 * r + 1] // nmb for r in range(nmb))
+
+
+@pytest.mark.parametrize("heads", [1, 2, 3, 4, 5, 6])
+def test_pair_order_visits_every_item_once(heads):
+    """Any number of whole heads per XCD: the split plan hands every row block out
+    exactly once (as one unit or as both pieces)."""
+    nmb = 9
+    n = NXCD * heads * nmb
+    item, piece, group, grid, ns = work_map(n, nmb, 64, 1)
+    seen = {}
+    for it, pc in zip(item, piece):
+        if it >= 0:
+            seen.setdefault(it, set()).add(pc)
+    assert sorted(seen) == list(range(n))
+    assert all(s == {0} or s == set(range(ns)) for s in seen.values())
 
 
 def test_workspace_size_follows_from_groups():
