@@ -113,13 +113,15 @@ int qik_attn_fwd(const qik_attn_args* args, void* stream);
 #define QIK_ATTN_WS_CTL_BYTES 32768
 
 /* Bytes of device workspace qik_attn_fwd_ws needs for `args` on the CURRENT
- * HIP device (0 only when there is no work).  The workspace holds control
- * words (queue heads, exit and arrival counts) and the partial softmax states
- * of split row blocks: the launch runs whole rounds of row blocks, then splits
- * each row block of the last, partly filled round over its KV tiles into two
- * pieces (seven tenths and three tenths of its tiles; halves when the launch
- * has no whole round and every piece gets a workgroup of its own) that the
- * second to finish combines.  The size depends on the shape and on the device's CU count only,
+ * HIP device (0 when there is no work, and when the launch has at most one
+ * row block per CU: then one workgroup of two 4-wave groups runs each row
+ * block, the groups taking the two halves of its KV tiles and combining them
+ * in LDS).  Otherwise the workspace holds control words (queue heads, exit and
+ * arrival counts) and the partial softmax states of split row blocks: the
+ * launch runs whole rounds of row blocks, then splits each row block of the
+ * last, partly filled round over its KV tiles into two pieces (seven tenths
+ * and three tenths of its tiles) that the second to finish combines.  The
+ * size depends on the shape and on the device's CU count only,
  * stays below 2 x (workgroups resident at once) x (BM x D x 4 + 2 KiB)
  * + 32 KiB (about 70 MB on MI355X, D = 128), and is about 41 MB for
  * Qwen-Image's 24-head, 4352-row layer.  Host-only (a cached device-attribute
@@ -129,9 +131,11 @@ int qik_attn_workspace_size(const qik_attn_args* args, int64_t* bytes);
 /* qik_attn_fwd for the whole device at once: the launch holds as many
  * workgroups as the device keeps resident, and they pull row blocks (and the
  * pieces of split row blocks) from one queue per XCD, so both workgroup
- * slots of every CU stay busy to the end.  Same arguments and tolerance as
- * qik_attn_fwd, bit-identical from run to run.  `workspace`: device memory of
- * the current device, 256-byte aligned, >= qik_attn_workspace_size bytes,
+ * slots of every CU stay busy to the end; a launch of at most one row block
+ * per CU runs the two-group form instead (one workgroup per row block, no
+ * workspace read: `workspace` may then be NULL).  Same arguments and
+ * tolerance as qik_attn_fwd, bit-identical from run to run.  `workspace`:
+ * device memory of the current device, 256-byte aligned, >= qik_attn_workspace_size bytes,
  * its first QIK_ATTN_WS_CTL_BYTES ZEROED ONCE before its first use (e.g.
  * hipMemset after allocating it); every launch leaves them zero again, so a
  * workspace is reused as is, also across shapes and by graph replays.  Launches that may overlap

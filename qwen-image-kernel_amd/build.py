@@ -30,6 +30,11 @@ HIPCC_FLAGS = [
     "-shared",
     # keep hipcc from forming packed-fp32 VALU ops (v_pk_*_f32)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # every device atomic here is issued by one thread; the atomic optimizer's
+    # wave-wide rewrite of such an atomic reads its return value at once,
+    # which would make the attention kernel wait out the queue draw's round
+    # trip where it means to overlap it with the unit's merge and store
+    "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
     "-Wall",
     "-Wno-unused-command-line-argument",
 ]

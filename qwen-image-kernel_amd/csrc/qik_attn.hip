@@ -207,6 +207,45 @@ __device__ __forceinline__ void wait_copies() { __builtin_amdgcn_s_waitcnt(0x0F7
 
 __device__ __forceinline__ u32x4 lds128(const char* p) { return *reinterpret_cast<const u32x4*>(p); }
 
+// Global-memory accesses through address-space-1 pointers.  Through a generic
+// pointer the compiler emits flat instructions, which count in lgkmcnt as well
+// as vmcnt: every later LDS or scalar-load wait (the causal-length reduction,
+// the kernel-argument loads of the next unit) then also waits for them, i.e.
+// for the Q rows from HBM or for the output stores to be acknowledged.
+typedef __attribute__((address_space(1))) unsigned gu32;
+__device__ __forceinline__ u32x4 gload16(const char* p) {
+  return *(const __attribute__((address_space(1))) u32x4*)p;
+}
+__device__ __forceinline__ int gload_i32(const int32_t* p) { return *(const __attribute__((address_space(1))) int32_t*)p; }
+__device__ __forceinline__ float gload_f32(const float* p) { return *(const __attribute__((address_space(1))) float*)p; }
+__device__ __forceinline__ void gstore8(char* p, u32x2 v) { *(__attribute__((address_space(1))) u32x2*)p = v; }
+__device__ __forceinline__ unsigned g_fetch_add(unsigned* p, unsigned v) {
+  return __hip_atomic_fetch_add((gu32*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned g_load(unsigned* p) {
+  return __hip_atomic_load((gu32*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void g_store(unsigned* p, unsigned v) {
+  __hip_atomic_store((gu32*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Wave-wide min or max of an int, returned as a wave-uniform value: four DPP
+// steps inside each 16-lane row (quad_perm 1,0,3,2; quad_perm 2,3,0,1;
+// row_half_mirror; row_mirror), after which every lane of a row holds the
+// row's result, then the four rows' lane 0 read as scalars.  No LDS round trip
+// (a __shfl_xor ladder is six ds_bpermute waits).
+template <bool MAX>
+__device__ __forceinline__ int wave_reduce_i32(int x) {
+  auto op = [](int a, int b) { return MAX ? max(a, b) : min(a, b); };
+  x = op(x, __builtin_amdgcn_update_dpp(x, x, 0xB1, 0xF, 0xF, false));
+  x = op(x, __builtin_amdgcn_update_dpp(x, x, 0x4E, 0xF, 0xF, false));
+  x = op(x, __builtin_amdgcn_update_dpp(x, x, 0x141, 0xF, 0xF, false));
+  x = op(x, __builtin_amdgcn_update_dpp(x, x, 0x140, 0xF, 0xF, false));
+  const int r0 = __builtin_amdgcn_readlane(x, 0), r1 = __builtin_amdgcn_readlane(x, 16);
+  const int r2 = __builtin_amdgcn_readlane(x, 32), r3 = __builtin_amdgcn_readlane(x, 48);
+  return op(op(r0, r1), op(r2, r3));
+}
+
 // Per-lane source offset (from the tile's first row) of the direct-to-LDS tile
 // copy.  Instruction r of wave w of a group fills LDS bytes [R0*ROWB, R0*ROWB +
 // 1024) with R0 = (1024/ROWB)*(NWAVES*r + w): lane l writes row R0 + l/CH,
@@ -263,8 +302,14 @@ __device__ __forceinline__ Params reread_args() {
   return p;
 }
 
-template <int D, bool FP16, bool V_FP8, bool KV>
-__global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params args) {
+// KSPLIT = 1: a workgroup of 4 waves runs one unit at a time (two workgroups
+// per CU).  KSPLIT = 2: a workgroup of two such groups of 4 waves, one per CU,
+// runs one row block: group 0 takes the first half of its KV tiles, group 1
+// the second, both through the same code with their own LDS stages, and
+// group 1 hands its partial state to group 0 through LDS at the end (the
+// launch for row blocks that fit the CUs once; no workspace, no queue).
+template <int D, bool FP16, bool V_FP8, bool KV, int KSPLIT>
+__global__ void __launch_bounds__(NTHREADS * KSPLIT, KSPLIT == 1 ? 2 : 1) attn_fwd_kernel(const Params args) {
   constexpr int CH = D / 8;              // 16-byte chunks per row (8 elements)
   constexpr int ROWB = D * 2;            // bytes per row of a K/V tile in LDS
   constexpr int KSTEPS = D / 16;         // k-steps of S^T = K.Q^T
@@ -279,21 +324,23 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params args
   static_assert(F8_LOADS >= 1 && F8_LOADS * NTHREADS * 16 == BN * D, "fp8 tile split");
   static_assert(BN == 64, "one key_valid byte per lane of wave 0");
 
-  __shared__ u32x4 sk0[TILE_BYTES / 16];
-  __shared__ u32x4 sk1[TILE_BYTES / 16];
-  __shared__ u32x4 sv0[TILE_BYTES / 16];
-  __shared__ u32x4 sv1[TILE_BYTES / 16];
-  __shared__ uint32_t skv[2][BN / 4];           // key_valid bytes of each stage's tile (4 per word)
-  __shared__ int skvall[2];                     // 1 when every key of the stage's tile is valid
-  __shared__ int sred[NWAVES];
+  static_assert(KSPLIT == 1 || KSPLIT == 2, "one or two groups of waves");
+  // per group: K stage 0, K stage 1, V stage 0, V stage 1 (one contiguous block)
+  __shared__ u32x4 stg[4 * KSPLIT][TILE_BYTES / 16];
+  __shared__ uint32_t skv[KSPLIT][2][BN / 4];   // key_valid bytes of each stage's tile (4 per word)
+  __shared__ int skvall[KSPLIT][2];             // 1 when every key of the stage's tile is valid
+  __shared__ int sred[KSPLIT][NWAVES];
   __shared__ int snext;                         // queue position handed out to this workgroup
-  char* const kst[2] = {reinterpret_cast<char*>(sk0), reinterpret_cast<char*>(sk1)};
-  char* const vst[2] = {reinterpret_cast<char*>(sv0), reinterpret_cast<char*>(sv1)};
+  __shared__ f32x2 sml[KSPLIT == 2 ? NTHREADS : 1];  // group 1's (m, l) at the merge
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
   // wave-uniform values go through readfirstlane so that the compiler keeps
   // them (and the buffer resources built from them) in SGPRs
+  const int grp = KSPLIT == 1 ? 0 : __builtin_amdgcn_readfirstlane((int)(threadIdx.x / NTHREADS));
+  char* const kst[2] = {reinterpret_cast<char*>(stg[4 * grp + 0]), reinterpret_cast<char*>(stg[4 * grp + 1])};
+  char* const vst[2] = {reinterpret_cast<char*>(stg[4 * grp + 2]), reinterpret_cast<char*>(stg[4 * grp + 3])};
+
+  const int tid = (int)threadIdx.x & (NTHREADS - 1);  // thread of the group
+  const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hf = lane >> 5;   // lane half: keys 4*hf.. of each 8-key group
   const int l32 = lane & 31;
@@ -310,16 +357,19 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params args
   const int nx = args.plan.nx;
   const int xcd = (int)(blockIdx.x % nx);
   const int gx = (int)(gridDim.x / nx);
-  int pend = -1;  // thread 0: the position drawn at the end of the last tile loop
+  // A position drawn at the end of a unit's tile loop (thread 0's `pend`) is
+  // written to snext just before that unit's output stores (or before it
+  // leaves the item to its other piece): its round trip overlaps the merge and
+  // the epilogue, and the next unit's head does not wait on it (loads and
+  // stores complete in issue order, so a wait there would also wait for the
+  // output stores to be acknowledged).
+  unsigned pend = 0;
+  bool drawn = false;
   for (int first = 1;; first = 0) {
     int bidv = (int)blockIdx.x;
     if (pulled) {
-      if (tid == 0) {
-        snext = pend >= 0 ? pend
-              : first ? (int)(blockIdx.x / nx)
-                      : gx + (int)__hip_atomic_fetch_add(args.ctl + xcd, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-      pend = -1;
+      if (tid == 0 && !drawn) snext = first ? (int)(blockIdx.x / nx) : gx + (int)g_fetch_add(args.ctl + xcd, 1u);
+      drawn = false;
       __syncthreads();
       const int loc = snext;
       __syncthreads();  // every thread has read snext before the next unit's head rewrites it
@@ -332,8 +382,12 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params args
     // unit: kept live across the unit loop instead, they crowd the SGPRs and
     // the scheduler then serialises the tile loop's LDS reads
     const Params p = reread_args();
-    const Work wk = plan_work(p.plan, bidv);
+    Work wk = plan_work(p.plan, bidv);
     if (wk.item < 0) continue;
+    if constexpr (KSPLIT == 2) {
+      wk.piece = grp;  // the groups are the row block's two pieces
+      wk.group = 0;
+    }
     const int vid = wk.item;
     const int nmb = p.plan.nmb;
     const int bh = vid / nmb;
@@ -344,44 +398,18 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params args
     const int m = mb * BM + wave * 32 + l32;  // this lane's query row
     const bool live = m < p.SQ;
 
-    // ---- causal lengths: this row's L; the block max (dead rows count as -1,
-    // triton_attention.py:82-83); the wave's min and max over live rows.
-    int Lrow = p.KV - 1;
-    if (!p.uniform) Lrow = live ? p.L[m] : -1;
-    int lmax = live ? Lrow : -1;
-    int lmin = live ? Lrow : INT_MAX;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-      lmax = max(lmax, __shfl_xor(lmax, off));
-      lmin = min(lmin, __shfl_xor(lmin, off));
-    }
-    if (lane == 0) sred[wave] = lmax;
-    __syncthreads();
-    int Lmax = sred[0];
-#pragma unroll
-    for (int w = 1; w < NWAVES; ++w) Lmax = max(Lmax, sred[w]);
-    Lmax = __builtin_amdgcn_readfirstlane(Lmax);
-    const int wave_minL = __builtin_amdgcn_readfirstlane(lmin);
-    const int wave_maxL = __builtin_amdgcn_readfirstlane(lmax);
-
-    // ---- KV-tile schedule: tile t of a segment starting at absolute key s0 is
-    // visited iff s0 + t*BN <= Lmax (segment-local tiles, triton_attention.py:97-124).
-    const int s1 = p.has_cache ? p.P : 0;
-    int run0 = 0;
-    if (p.has_cache && Lmax >= 0) run0 = min(cdiv_i(p.P, BN), Lmax / BN + 1);
-    int run1 = 0;
-    if (Lmax >= s1) run1 = min(cdiv_i(p.SN, BN), (Lmax - s1) / BN + 1);
-    const int T = run0 + run1;
-
-    if (p.debug_tiles != nullptr && tid == 0 && wk.piece == 0) p.debug_tiles[bh * nmb + mb] = T;
-
-    // ---- this unit's tiles [g0, g1): all of them, or one of the item's two
-    // pieces (T, and so the split, is the same for both pieces of the item)
-    const bool split = wk.group >= 0 && T >= SPLIT_MIN_TILES;
-    if (wk.piece > 0 && !split) continue;
-    const int gsplit = p.plan.even ? (T + 1) / 2 : (7 * T + 5) / 10;
-    const int g0 = (split && wk.piece) ? gsplit : 0;
-    const int g1 = (split && !wk.piece) ? gsplit : T;
+    // ---- the unit's memory reads go out first, in this order: the row's
+    // causal length, Q, then the first tile's copies when the unit's first
+    // tile is known before the lengths are reduced.  Loads complete in issue
+    // order, so the wait for L then covers Q as well but not the copies.
+    // Dead rows of the last row block read row SQ-1 instead: the loads need
+    // no branch around them (the compiler then counts them and waits for L
+    // alone); a dead row's L is -1 below and its results are never stored.
+    const int mrd = live ? m : p.SQ - 1;
+    // (with uniform lengths there is no L: the load reads a Q word instead and
+    // its value is never used; an unconditional load keeps the compiler from
+    // ordering a wait before it)
+    const int Lraw = gload_i32(p.uniform ? reinterpret_cast<const int32_t*>(p.q) : p.L + mrd);
 
     // ---- per-(b,h) segment bases (bytes) and row strides
     constexpr int VC_ES = V_FP8 ? 1 : 2;
@@ -394,11 +422,19 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params args
     if (p.has_cache) {
       kcb = p.k_cache + (b * p.skc[0] + h * p.skc[2]) * 2;
       vcb = p.v_cache + (b * p.svc[0] + h * p.svc[2]) * VC_ES;
-      if constexpr (V_FP8) vsc = p.v_scale[b * p.H + h];
+      if constexpr (V_FP8) vsc = gload_f32(p.v_scale + b * p.H + h);
     }
     const int kns = (int)(p.skn[1] * 2), vns = (int)(p.svn[1] * 2);
     const int kcs = (int)(p.skc[1] * 2), vcs = (int)(p.svc[1] * VC_ES);
     const float qk_scale = p.qk_scale;
+
+    // ---- Q as the B operand of S^T = K.Q^T: lane holds Q[m, 16j + 8hf .. +8]
+    u32x4 qreg[KSTEPS];
+    {
+      const char* qr = qb + (int64_t)mrd * p.sq[1] * 2;
+#pragma unroll
+      for (int j = 0; j < KSTEPS; ++j) qreg[j] = gload16(qr + (16 * j + 8 * hf) * 2);
+    }
 
     // lane offsets of the tile copies, per segment and tensor
     const uint32_t koff_new = dma_lane_offset<D>(lane, wave, kns);
@@ -408,41 +444,14 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params args
       koff_c = dma_lane_offset<D>(lane, wave, kcs);
       if constexpr (!V_FP8) voff_c = dma_lane_offset<D>(lane, wave, vcs);
     }
-
-    // ---- Q as the B operand of S^T = K.Q^T: lane holds Q[m, 16j + 8hf .. +8]
-    u32x4 qreg[KSTEPS];
-    {
-      const char* qr = qb + (int64_t)m * p.sq[1] * 2;
-#pragma unroll
-      for (int j = 0; j < KSTEPS; ++j) {
-        qreg[j] = live ? *reinterpret_cast<const u32x4*>(qr + (16 * j + 8 * hf) * 2)
-                       : u32x4{0u, 0u, 0u, 0u};
-      }
-    }
-
-    // ---- LDS operand offsets inside a stage (lane constants)
-    const int swk = swz<CH>(l32);  // rows l32 and l32 + 32 share it
-    int koffs[KSTEPS];
-#pragma unroll
-    for (int j = 0; j < KSTEPS; ++j) koffs[j] = l32 * ROWB + (((2 * j + hf) ^ swk) << 4);
-    const int j16 = lane & 15;
-    const int rq = 4 * hf + (j16 >> 2);   // V^T read rows: 32*(s>>1) + 16*(s&1) + rq (+8)
-    const int colq = 16 * ((lane >> 4) & 1) + 4 * (j16 & 3);
-    int voffs[2][DBLK];
-#pragma unroll
-    for (int db = 0; db < DBLK; ++db) {
-      const int col = db * 32 + colq;
-      voffs[0][db] = rq * ROWB + (((col >> 3) ^ swz<CH>(rq)) << 4) + ((col & 7) << 1);
-      voffs[1][db] = (rq + 8) * ROWB + (((col >> 3) ^ swz<CH>(rq + 8)) << 4) + ((col & 7) << 1);
-    }
+    const int s1 = p.has_cache ? p.P : 0;  // absolute index of the first fresh key
 
     // fp8 slab V goes through registers: two 16-fp8 chunks per thread per tile
     u32x4 f8reg[F8_LOADS];
     uint32_t kvbyte = 0;
 
-    auto issue_tile = [&](int g, int stage) {
-      const bool seg0 = g < run0;
-      const int t = seg0 ? g : g - run0;
+    // copies of tile t of the slab (seg0) or of the fresh keys into `stage`
+    auto issue_seg = [&](bool seg0, int t, int stage) {
       const int row0 = t * BN;
       const int n_in = (seg0 ? p.P : p.SN) - row0;
       char* kd = kst[stage];
@@ -478,6 +487,88 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params args
         if (tid < BN) kvbyte = __builtin_amdgcn_raw_buffer_load_b8(rs, (uint32_t)tid, 0, 0);
       }
     };
+
+    // ---- causal lengths: the block max (dead rows count as -1,
+    // triton_attention.py:82-83); the wave's min and max over live rows.
+    // With uniform lengths every live row has L = KV - 1 and nothing is read.
+    const bool wave_live = mb * BM + wave * 32 < p.SQ;
+    int Lrow = p.KV - 1;  // this row's causal length
+    int Lmax = p.KV - 1;
+    int wave_minL = wave_live ? p.KV - 1 : INT_MAX;
+    int wave_maxL = wave_live ? p.KV - 1 : -1;
+    // A first piece starts at tile 0 whatever the lengths are (the slab's
+    // first tile with a cache, else the fresh keys' first): its copies go out
+    // before the lengths are reduced.  With uniform lengths every unit's
+    // tiles are known here.
+    const bool early = p.uniform || wk.piece == 0;
+    int run0 = 0, run1 = 0;
+    auto schedule = [&]() {
+      // KV-tile schedule: tile t of a segment starting at absolute key s0 is
+      // visited iff s0 + t*BN <= Lmax (segment-local tiles, triton_attention.py:97-124)
+      run0 = (p.has_cache && Lmax >= 0) ? min(cdiv_i(p.P, BN), Lmax / BN + 1) : 0;
+      run1 = (Lmax >= s1) ? min(cdiv_i(p.SN, BN), (Lmax - s1) / BN + 1) : 0;
+    };
+    auto piece_tiles = [&](int T, int& g0, int& g1) {
+      // this unit's tiles [g0, g1): all of them, or one of the item's two
+      // pieces (T, and so the split, is the same for both pieces of the item);
+      // a second group with nothing to do gets an empty range
+      const bool split = wk.group >= 0 && T >= SPLIT_MIN_TILES;
+      const int gsplit = (KSPLIT == 2 || p.plan.even) ? (T + 1) / 2 : (7 * T + 5) / 10;
+      g0 = (split && wk.piece) ? gsplit : 0;
+      g1 = (split && !wk.piece) ? gsplit : T;
+      if (KSPLIT == 2 && !split && wk.piece) g0 = T;
+      return split;
+    };
+    if (p.uniform) {
+      schedule();
+      int e0, e1;
+      piece_tiles(run0 + run1, e0, e1);
+      if (e0 < e1) {
+        const bool seg0 = e0 < run0;
+        issue_seg(seg0, seg0 ? e0 : e0 - run0, 0);
+      }
+    } else {
+      if (wk.piece == 0) issue_seg(p.has_cache != 0, 0, 0);
+      Lrow = live ? Lraw : -1;
+      const int lmax = wave_reduce_i32<true>(live ? Lrow : -1);
+      wave_minL = wave_reduce_i32<false>(live ? Lrow : INT_MAX);
+      wave_maxL = lmax;
+      if (lane == 0) sred[grp][wave] = lmax;
+      __syncthreads();
+      Lmax = sred[grp][0];
+#pragma unroll
+      for (int w = 1; w < NWAVES; ++w) Lmax = max(Lmax, sred[grp][w]);
+      Lmax = __builtin_amdgcn_readfirstlane(Lmax);
+      schedule();
+    }
+    const int T = run0 + run1;
+
+    if (p.debug_tiles != nullptr && tid == 0 && wk.piece == 0) p.debug_tiles[bh * nmb + mb] = T;
+
+    int g0, g1;
+    const bool split = piece_tiles(T, g0, g1);
+    if (KSPLIT == 1 && wk.piece > 0 && !split) continue;
+
+    // ---- LDS operand offsets inside a stage (lane constants)
+    const int swk = swz<CH>(l32);  // rows l32 and l32 + 32 share it
+    int koffs[KSTEPS];
+#pragma unroll
+    for (int j = 0; j < KSTEPS; ++j) koffs[j] = l32 * ROWB + (((2 * j + hf) ^ swk) << 4);
+    const int j16 = lane & 15;
+    const int rq = 4 * hf + (j16 >> 2);   // V^T read rows: 32*(s>>1) + 16*(s&1) + rq (+8)
+    const int colq = 16 * ((lane >> 4) & 1) + 4 * (j16 & 3);
+    int voffs[2][DBLK];
+#pragma unroll
+    for (int db = 0; db < DBLK; ++db) {
+      const int col = db * 32 + colq;
+      voffs[0][db] = rq * ROWB + (((col >> 3) ^ swz<CH>(rq)) << 4) + ((col & 7) << 1);
+      voffs[1][db] = (rq + 8) * ROWB + (((col >> 3) ^ swz<CH>(rq + 8)) << 4) + ((col & 7) << 1);
+    }
+
+    auto issue_tile = [&](int g, int stage) {
+      const bool seg0 = g < run0;
+      issue_seg(seg0, seg0 ? g : g - run0, stage);
+    };
     // register-staged parts of a tile: fp8 V dequantised to bf16, key_valid bytes
     auto finish_tile = [&](int g, int stage) {
       char* vd = vst[stage];
@@ -497,9 +588,9 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params args
       }
       if (KV && tid < BN) {
         // wave 0 holds the tile's BN bytes, one per lane
-        reinterpret_cast<uint8_t*>(skv[stage])[tid] = (uint8_t)kvbyte;
+        reinterpret_cast<uint8_t*>(skv[grp][stage])[tid] = (uint8_t)kvbyte;
         const int allv = __all(kvbyte != 0u);
-        if (tid == 0) skvall[stage] = allv;
+        if (tid == 0) skvall[grp][stage] = allv;
       }
     };
 
@@ -542,14 +633,14 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params args
       // mask: segment tail, kv <= L[row], key_valid (triton_attention.py:126-144)
       // a tile whose keys are all valid needs no key_valid term (tail tiles are
       // never all valid: bytes past the segment end read as 0)
-      const bool kv_mask = KV && __builtin_amdgcn_readfirstlane(skvall[stage]) == 0;
+      const bool kv_mask = KV && __builtin_amdgcn_readfirstlane(skvall[grp][stage]) == 0;
       const bool full = (n_in >= BN) && (kv0 + BN - 1 <= wave_minL) && !kv_mask;
       if (!full) {
         const int lim = min(Lrow - kv0, n_in - 1) - 4 * hf;  // allowed: n_local - 4hf <= lim
         uint32_t kvw[8];
         if (kv_mask) {
 #pragma unroll
-          for (int q = 0; q < 8; ++q) kvw[q] = skv[stage][q * 2 + hf];  // bytes of keys 8q + 4hf .. +3
+          for (int q = 0; q < 8; ++q) kvw[q] = skv[grp][stage][q * 2 + hf];  // bytes of keys 8q + 4hf .. +3
         }
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
@@ -622,25 +713,46 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params args
     };
 
     if (g0 < g1) {
-      issue_tile(g0, 0);
+      if (!early) issue_tile(g0, 0);
       finish_tile(g0, 0);
     }
     wait_copies();
     __syncthreads();
 
-    for (int g = g0; g < g1; g += 2) {
-      // tiles g0, g0 + 2, ... from stage 0, the others from stage 1 (constant LDS offsets)
-      if (g + 1 < g1) issue_tile(g + 1, 1);
-      compute_tile(g, 0);
-      if (g + 1 < g1) finish_tile(g + 1, 1);
-      wait_copies();
-      __syncthreads();
-      if (g + 1 < g1) {
-        if (g + 2 < g1) issue_tile(g + 2, 0);
-        compute_tile(g + 1, 1);
-        if (g + 2 < g1) finish_tile(g + 2, 0);
+    if constexpr (KSPLIT == 1) {
+      for (int g = g0; g < g1; g += 2) {
+        // tiles g0, g0 + 2, ... from stage 0, the others from stage 1 (constant LDS offsets)
+        if (g + 1 < g1) issue_tile(g + 1, 1);
+        compute_tile(g, 0);
+        if (g + 1 < g1) finish_tile(g + 1, 1);
         wait_copies();
         __syncthreads();
+        if (g + 1 < g1) {
+          if (g + 2 < g1) issue_tile(g + 2, 0);
+          compute_tile(g + 1, 1);
+          if (g + 2 < g1) finish_tile(g + 2, 0);
+          wait_copies();
+          __syncthreads();
+        }
+      }
+    } else {
+      // both groups step through group 0's tile count (group 1 has at most as
+      // many) so that they reach every barrier together
+      const int nsteps = split ? (T + 1) / 2 : T;
+      for (int st = 0; st < nsteps; st += 2) {
+        const int g = g0 + st;
+        if (g + 1 < g1) issue_tile(g + 1, 1);
+        if (g < g1) compute_tile(g, 0);
+        if (g + 1 < g1) finish_tile(g + 1, 1);
+        wait_copies();
+        __syncthreads();
+        if (st + 1 < nsteps) {
+          if (g + 2 < g1) issue_tile(g + 2, 0);
+          if (g + 1 < g1) compute_tile(g + 1, 1);
+          if (g + 2 < g1) finish_tile(g + 2, 0);
+          wait_copies();
+          __syncthreads();
+        }
       }
     }
 
@@ -665,9 +777,44 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params args
     // L2 invalidate of the whole XCD, which throws away the other workgroups'
     // K/V lines (measured: the first version was 30% slower with it).
     const Params pe = reread_args();
-    if (pulled && tid == 0) pend = gx + (int)__hip_atomic_fetch_add(pe.ctl + xcd, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (pulled && tid == 0) pend = g_fetch_add(pe.ctl + xcd, 1u);
+    drawn = pulled;
     float l_part = l_run;
-    if (split) {
+    if constexpr (KSPLIT == 2) {
+      if (split) {
+        // group 1 hands its O^T accumulators and (m, l) to group 0 through
+        // its own stage block (free: the tile loop ended with a barrier), and
+        // group 0 combines the two in piece order, the arithmetic of the
+        // merge through the workspace below
+        f32x4* const xs = reinterpret_cast<f32x4*>(stg[4]);
+        if (grp == 1) {
+#pragma unroll
+          for (int db = 0; db < DBLK; ++db)
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4)
+              xs[(db * 4 + q4) * NTHREADS + tid] =
+                  f32x4{oacc[db][4 * q4 + 0], oacc[db][4 * q4 + 1], oacc[db][4 * q4 + 2], oacc[db][4 * q4 + 3]};
+          sml[tid] = f32x2{m_run, l_run};
+        }
+        __syncthreads();
+        if (grp == 0) {
+          const f32x2 mlo = sml[tid];
+          const float m0 = m_run, m1 = mlo[0];
+          const float mm = fmaxf(m0, m1);
+          const float a0 = (m0 == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m0 - mm);
+          const float a1 = (m1 == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m1 - mm);
+          l_part = l_run * a0 + mlo[1] * a1;
+#pragma unroll
+          for (int db = 0; db < DBLK; ++db)
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+              const f32x4 v = xs[(db * 4 + q4) * NTHREADS + tid];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) oacc[db][4 * q4 + e] = oacc[db][4 * q4 + e] * a0 + v[e] * a1;
+            }
+        }
+      }
+    } else if (split) {
       constexpr int OB = slot_oacc_bytes<D>();
       constexpr int SB = slot_bytes<D>();
       constexpr int SC1 = 16;  // cache policy: device scope
@@ -677,12 +824,12 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params args
       // it back).  A piece that finds the other one already arrived merges
       // at once and never writes its own slot; otherwise it publishes its
       // slot and arrives, and the second to arrive merges.
-      if (tid == 0) sred[0] = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 1u ? 1 : 0;
+      if (tid == 0) sred[0][0] = g_load(word) == 1u ? 1 : 0;
       __syncthreads();
-      const bool other_first = sred[0] != 0;
-      __syncthreads();  // every thread has read sred[0] before it is reused
+      const bool other_first = sred[0][0] != 0;
+      __syncthreads();  // every thread has read the flag before it is reused
       if (other_first) {
-        if (tid == 0) __hip_atomic_store(word, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (tid == 0) g_store(word, 0u);
       } else {
         const auto mine = make_rsrc(gslots + wk.piece * SB, SB);
 #pragma unroll
@@ -698,13 +845,14 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params args
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the slot has reached device scope
         __syncthreads();
         if (tid == 0) {
-          const unsigned before = __hip_atomic_fetch_add(word, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          const unsigned before = g_fetch_add(word, 1u);
           const bool last = before == 1u;
-          if (last) __hip_atomic_store(word, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          sred[0] = last ? 1 : 0;
+          if (last) g_store(word, 0u);
+          sred[0][0] = last ? 1 : 0;
         }
+        if (pulled && tid == 0) snext = gx + (int)pend;
         __syncthreads();
-        if (sred[0] == 0) continue;  // not the last piece: the last one finishes the item
+        if (sred[0][0] == 0) continue;  // not the last piece: the last one finishes the item
       }
 
       // the other piece's state; the two combine in piece order, the same
@@ -737,7 +885,8 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params args
     // ---- epilogue: out = l > 0 ? acc / l : 0 (triton_attention.py:166-168)
     const float l_tot = pair_sum(l_part);
     const float inv = (l_tot > 0.0f) ? 1.0f / l_tot : 0.0f;
-    if (live) {
+    if (pulled && tid == 0) snext = gx + (int)pend;
+    if (live && grp == 0) {
       char* orow = pe.out + (b * pe.so[0] + (int64_t)m * pe.so[1] + h * pe.so[2]) * 2;
 #pragma unroll
       for (int db = 0; db < DBLK; ++db)
@@ -747,7 +896,7 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params args
           u32x2 w;
           w.x = pack2<FP16>(oacc[db][4 * q4 + 0] * inv, oacc[db][4 * q4 + 1] * inv);
           w.y = pack2<FP16>(oacc[db][4 * q4 + 2] * inv, oacc[db][4 * q4 + 3] * inv);
-          *reinterpret_cast<u32x2*>(orow + d * 2) = w;
+          gstore8(orow + d * 2, w);
         }
     }
   }  // units
@@ -756,10 +905,10 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(const Params args
   // (every workgroup of the XCD has drawn its last position by then)
   if (pulled && tid == 0) {
     const unsigned g = gridDim.x / nx;
-    const unsigned before = __hip_atomic_fetch_add(args.ctl + NXCD_MAX + xcd, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned before = g_fetch_add(args.ctl + NXCD_MAX + xcd, 1u);
     if (before == g - 1) {
-      __hip_atomic_store(args.ctl + xcd, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(args.ctl + NXCD_MAX + xcd, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      g_store(args.ctl + xcd, 0u);
+      g_store(args.ctl + NXCD_MAX + xcd, 0u);
     }
   }
 }
@@ -802,18 +951,19 @@ __global__ void zero16_kernel(u32x4* p, int n16) {
 
 typedef void (*kernel_fn)(Params);
 
-template <int D, bool KV>
+template <int D, bool KV, int KS>
 kernel_fn pick_kernel(bool fp16, bool vfp8) {
-  if (fp16) return attn_fwd_kernel<D, true, false, KV>;
-  if (vfp8) return attn_fwd_kernel<D, false, true, KV>;
-  return attn_fwd_kernel<D, false, false, KV>;
+  if (fp16) return attn_fwd_kernel<D, true, false, KV, KS>;
+  if (vfp8) return attn_fwd_kernel<D, false, true, KV, KS>;
+  return attn_fwd_kernel<D, false, false, KV, KS>;
 }
 
 // key_valid is a template parameter: without a mask the kernel carries none
 // of its code (the tile loop is then the same as with no mask support at all)
 template <int D>
-kernel_fn pick_kernel(bool fp16, bool vfp8, bool kv) {
-  return kv ? pick_kernel<D, true>(fp16, vfp8) : pick_kernel<D, false>(fp16, vfp8);
+kernel_fn pick_kernel(bool fp16, bool vfp8, bool kv, bool two_groups) {
+  if (two_groups) return kv ? pick_kernel<D, true, 2>(fp16, vfp8) : pick_kernel<D, false, 2>(fp16, vfp8);
+  return kv ? pick_kernel<D, true, 1>(fp16, vfp8) : pick_kernel<D, false, 1>(fp16, vfp8);
 }
 
 inline bool aligned_to(const void* ptr, uintptr_t a) { return (reinterpret_cast<uintptr_t>(ptr) % a) == 0; }
@@ -841,6 +991,21 @@ int schedule_one(int64_t Lmax, int64_t P, int64_t SN, bool has_cache) {
 constexpr int MAX_DEVICES = 64;
 std::atomic<int> g_slots[MAX_DEVICES][12];
 std::atomic<int> g_xcds[MAX_DEVICES];
+std::atomic<int> g_cus[MAX_DEVICES];
+
+// Compute units of the current device, cached per device (0 if unknown).
+int device_cus() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (dev >= 0 && dev < MAX_DEVICES) {
+    const int c = g_cus[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) return 0;
+  if (dev >= 0 && dev < MAX_DEVICES) g_cus[dev].store(cus, std::memory_order_relaxed);
+  return cus;
+}
 
 // XCDs of the current device (hipDeviceAttributeNumberOfXccs; NXCD if the
 // runtime cannot say), clamped to [1, NXCD_MAX], cached per device.
@@ -894,6 +1059,7 @@ struct Launch {
   kernel_fn fn;
   WorkPlan plan;
   int64_t grid;
+  int threads;         // per workgroup: NTHREADS, or 2 * NTHREADS for the two-group kernel
   int64_t ws_bytes;    // 0: no workspace
   int64_t ctl_bytes;   // control words at the start of the workspace
   int slot;
@@ -905,15 +1071,25 @@ int plan_launch(const qik_attn_args* a, bool split, Launch* L) {
   const bool fp16 = a->dtype == QIK_DTYPE_FP16;
   const bool vfp8 = (a->flags & QIK_V_CACHE_FP8) != 0;
   const bool kv = (a->flags & QIK_HAS_KEY_VALID) != 0;
-  L->fn = (a->D == 128) ? pick_kernel<128>(fp16, vfp8, kv) : pick_kernel<64>(fp16, vfp8, kv);
+  L->fn = (a->D == 128) ? pick_kernel<128>(fp16, vfp8, kv, false) : pick_kernel<64>(fp16, vfp8, kv, false);
   L->slot = (a->D == 128) ? slot_bytes<128>() : slot_bytes<64>();
   L->ws_bytes = 0;
   L->ctl_bytes = 0;
   L->grid = 0;
+  L->threads = NTHREADS;
   memset(&L->plan, 0, sizeof(L->plan));
   if (n == 0) return QIK_OK;
   const int nx = device_xcds();
   int sx = 1;
+  if (split && n <= device_cus()) {
+    // row blocks fit the CUs once: one two-group workgroup per row block, its
+    // KV tiles split between the groups and merged in LDS (no workspace)
+    L->fn = (a->D == 128) ? pick_kernel<128>(fp16, vfp8, kv, true) : pick_kernel<64>(fp16, vfp8, kv, true);
+    L->threads = 2 * NTHREADS;
+    L->plan = make_plan((int)n, (int)nmb, 1, 0, 1, nx);
+    L->grid = (int64_t)nx * L->plan.wpx;
+    return QIK_OK;
+  }
   if (split) {
     const int st = slots_per_xcd(L->fn, pick_index((int)a->D, fp16, vfp8, kv), &sx);
     if (st != QIK_OK) return st;
@@ -997,7 +1173,7 @@ int launch(const qik_attn_args* a, bool split, void* ws, int64_t ws_bytes, void*
 
   void* kargs[] = {&p};
   const hipError_t e = hipLaunchKernel(reinterpret_cast<const void*>(L.fn), dim3((unsigned)L.grid),
-                                       dim3(NTHREADS), kargs, 0, static_cast<hipStream_t>(stream));
+                                       dim3((unsigned)L.threads), kargs, 0, static_cast<hipStream_t>(stream));
   return e == hipSuccess ? QIK_OK : QIK_ERR_LAUNCH;
 }
 

@@ -1,16 +1,21 @@
-"""GPU parity of the split last round (qik_attn_fwd_ws).
+"""GPU parity of the split launches of qik_attn_fwd_ws.
 
-Each row block of a launch's last, partly filled round runs as two pieces
-over interleaved KV tiles, which meet in a workspace, and the launch's
-resident workgroups pull their units from per-XCD queues.  Checked here
-against the CPU oracle (same bars as the unsplit kernel: max-abs 2e-2,
-mean-abs 2e-3), against the unsplit launch, run to run (bit-identical), with
-rows that see no key in one piece or in any, with garbage in the slots, with
-the control words back at zero after every launch, under HIP-graph replay,
-and the host-side workspace checks.
+Two forms, chosen by the number of row blocks n:
+* n above the CU count: each row block of the launch's last, partly filled
+  round runs as two pieces over its KV tiles, which meet in a workspace, and
+  the launch's resident workgroups pull their units from per-XCD queues;
+* n at most the CU count: one workgroup of two 4-wave groups per row block,
+  the groups taking the two halves of its KV tiles and merging in LDS (no
+  workspace).
+Checked here against the CPU oracle (same bars as the unsplit kernel: max-abs
+2e-2, mean-abs 2e-3), against the unsplit launch, run to run (bit-identical),
+with rows that see no key in one piece or in any, with garbage in the slots,
+with the control words back at zero after every launch, under HIP-graph
+replay, and the host-side workspace checks.
 """
 
 import ctypes
+import dataclasses
 
 import numpy as np
 import pytest
@@ -67,17 +72,33 @@ def _ctl_bytes(ngroups):
     return CTL_BYTES
 
 
+def _cus():
+    return torch.cuda.get_device_properties(0).multi_processor_count
+
+
 def _n_groups(args):
-    """Split row blocks of one launch on this device, checked against the workspace size."""
+    """Row blocks of one launch on this device that merge through the workspace,
+    checked against the workspace size; 0 for the two-group form (no workspace)."""
     nmb = -(-args.SQ // 128)
+    if args.B * args.H * nmb <= _cus():
+        assert _ws_bytes(args) == 0
+        return 0
     ngroups, ns = _plan(args.B * args.H * nmb, nmb)
     slot = 128 * args.D * 4 + 256 * 8
     assert _ws_bytes(args) == _ctl_bytes(ngroups) + ngroups * ns * slot
     return ngroups
 
 
+def _workload(name):
+    """A benchmark workload, or ``t2i_512_b2``: the 512px layer with two batches
+    (432 row blocks, more than the CUs: the queue and the workspace merge)."""
+    if name == "t2i_512_b2":
+        return dataclasses.replace(wls.workload("t2i_512"), name=name, B=2)
+    return wls.workload(name)
+
+
 def _prefill(name, seed):
-    wl = wls.workload(name)
+    wl = _workload(name)
     inp = wls.make_inputs(wl, seed=seed, device=DEV, gen_device="cuda")
     return wl, inp
 
@@ -98,8 +119,8 @@ def test_workspace_size_matches_the_device_plan():
     assert _n_groups(a) > 0
 
 
-@pytest.mark.parametrize("name", ["t2i_512", "multiref_cfg"])
-def test_split_vs_unsplit_vs_oracle(name):
+@pytest.mark.parametrize("name,workspace", [("t2i_512", False), ("t2i_512_b2", True), ("multiref_cfg", True)])
+def test_split_vs_unsplit_vs_oracle(name, workspace):
     _flush(f"case split {name}")
     wl, inp = _prefill(name, seed=11)
     a = _run(wl, inp, True)
@@ -107,11 +128,11 @@ def test_split_vs_unsplit_vs_oracle(name):
     torch.cuda.synchronize()
     args = make_args(inp["query"], inp["key"], inp["value"], inp["prefix_lengths"], None, a,
                      inp["cache_k"], inp["cache_v"], inp["cache_v_scale"], wl.uniform)
-    assert _n_groups(args) > 0
+    assert (_n_groups(args) > 0) == workspace
     d = (a.float() - b.float()).abs()
     # both within the oracle bar below; between them only the accumulation order differs
     assert d.max().item() <= 2 * MAX_ABS and d.mean().item() <= 5e-4, (d.max().item(), d.mean().item())
-    heads = list(range(wl.H)) if name == "t2i_512" else [3, 17]
+    heads = list(range(wl.H)) if wl.B == 1 and wl.P == 0 else [3, 17]
     slab = {} if wl.P == 0 else dict(cache_k=inp["cache_k"].cpu(), cache_v=inp["cache_v"].cpu(),
                                      cache_v_scale=inp["cache_v_scale"].cpu())
     ref = oa.attention_fp32(inp["query"].cpu(), inp["key"].cpu(), inp["value"].cpu(), wl.lengths(), None,
@@ -121,35 +142,38 @@ def test_split_vs_unsplit_vs_oracle(name):
         _check(b[:, :, h], ref[:, :, h], f"{name} h{h} unsplit")
 
 
+@pytest.mark.parametrize("H", [4, 32])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("D", [64, 128])
-def test_split_dtypes_and_head_dims(dtype, D):
+def test_split_dtypes_and_head_dims(dtype, D, H):
     """128 text + 1024 image rows over 1152 keys: 18 KV tiles per image row block, so
-    every row block of this one-round launch is split and merged (both pieces
-    non-empty), in both element types and both head dims."""
-    _flush(f"case split dtype={dtype} D={D}")
-    g = torch.Generator().manual_seed(30 + D)
-    segs = [(0, 128, True), (128, 1152, False)]
-    S, H = 1152, 4
+    every image row block of this one-round launch is split and merged (both pieces
+    non-empty), in both element types and both head dims; 4 heads (36 row blocks)
+    take the two-group form, 32 heads (288) the queue and the workspace."""
+    _flush(f"case split dtype={dtype} D={D} H={H}")
+    g = torch.Generator().manual_seed(30 + D + H)
+    S = 1152
     q, k, v = ((torch.randn(1, S, H, D, generator=g)).to(dtype) for _ in range(3))
     L = np.arange(S, dtype=np.int32)
     L[128:] = S - 1
     Ld = torch.from_numpy(L).to(DEV)
     out = qik.block_causal_flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), Ld, None)
     args = make_args(q.to(DEV), k.to(DEV), v.to(DEV), Ld, None, out, None, None, None, False)
-    assert _n_groups(args) > 0
+    assert (_n_groups(args) > 0) == (H * 9 > _cus())
     assert out.dtype == dtype
     _check(out, oa.attention_fp32(q, k, v, L), f"{dtype} D={D}")
     again = qik.block_causal_flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), Ld, None)
     assert torch.equal(out, again)
 
 
-def test_split_decode_against_fp8_slab():
+@pytest.mark.parametrize("H", [3, 48])
+def test_split_decode_against_fp8_slab(H):
     """Decode of 640 target rows against a 512-row fp8 slab + 640 fresh keys (18 tiles,
-    the first 8 from the slab): the split row blocks mix slab and fresh tiles."""
-    _flush("case split fp8 slab decode")
-    g = torch.Generator().manual_seed(40)
-    B, P, SN, H, D = 2, 512, 640, 3, 128
+    the first 8 from the slab): the split row blocks mix slab and fresh tiles (3 heads:
+    the two-group form; 48 heads, 480 row blocks: the workspace merge)."""
+    _flush(f"case split fp8 slab decode H={H}")
+    g = torch.Generator().manual_seed(40 + H)
+    B, P, SN, D = 2, 512, 640, 128
     pk, pv = ((torch.randn(B, P, H, D, generator=g)).to(torch.bfloat16) for _ in range(2))
     q, k, v = ((torch.randn(B, SN, H, D, generator=g)).to(torch.bfloat16) for _ in range(3))
     cache = qik.ContiguousKVCache(1, B, P + 64, H, D, v_fp8=True, device=DEV)
@@ -159,26 +183,29 @@ def test_split_decode_against_fp8_slab():
     out = qik.block_causal_flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), L, None, cache_k=kc, cache_v=vc,
                                            cache_v_scale=sc, uniform_full=True)
     args = make_args(q.to(DEV), k.to(DEV), v.to(DEV), None, None, out, kc, vc, sc, True)
-    assert _n_groups(args) > 0
+    assert (_n_groups(args) > 0) == (B * H * 5 > _cus())
     ref = oa.attention_fp32(q, k, v, L.cpu().numpy(), None, kc.cpu(), vc.cpu(), sc.cpu())
     _check(out, ref, "fp8 slab decode")
 
 
-def test_split_is_bit_identical_run_to_run():
+@pytest.mark.parametrize("name", ["t2i_512", "t2i_512_b2"])
+def test_split_is_bit_identical_run_to_run(name):
     """Whichever piece arrives last merges, in piece order: the result never changes."""
-    _flush("case split determinism")
-    wl, inp = _prefill("t2i_512", seed=12)
+    _flush(f"case split determinism {name}")
+    wl, inp = _prefill(name, seed=12)
     outs = [_run(wl, inp, True) for _ in range(4)]
     for o in outs[1:]:
         assert torch.equal(outs[0], o)
 
 
-def test_rows_without_keys_in_one_piece_or_any():
+@pytest.mark.parametrize("H", [3, 48])
+def test_rows_without_keys_in_one_piece_or_any(H):
     """1024 keys = 16 tiles, two pieces of 8: rows with L < 512 see nothing in piece 1,
-    rows with L = -1 nothing at all (zeros); key_valid clears piece 0 for batch 1."""
-    _flush("case split empty halves")
+    rows with L = -1 nothing at all (zeros); key_valid clears piece 0 for batch 1
+    (3 heads: the two-group form; 48 heads: the workspace merge)."""
+    _flush(f"case split empty halves H={H}")
     g = torch.Generator().manual_seed(13)
-    B, SQ, SN, H, D = 2, 640, 1024, 3, 128
+    B, SQ, SN, D = 2, 640, 1024, 128
     q, k, v = (_rand((B, n, H, D), g) for n in (SQ, SN, SN))
     rng = np.random.default_rng(13)
     L = rng.integers(-1, SN, size=SQ).astype(np.int32)
@@ -194,7 +221,7 @@ def test_rows_without_keys_in_one_piece_or_any():
     a = qik.block_causal_flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), Ld, kv.to(DEV))
     b = qik.block_causal_flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), Ld, kv.to(DEV), split_tail=False)
     args = make_args(q.to(DEV), k.to(DEV), v.to(DEV), Ld, kv.to(DEV).to(torch.uint8), a, None, None, None, False)
-    assert _n_groups(args) > 0
+    assert (_n_groups(args) > 0) == (B * H * 5 > _cus())
     ref = oa.attention_fp32(q, k, v, L, kv.numpy())
     _check(a, ref, "split")
     _check(b, ref, "unsplit")
@@ -210,7 +237,7 @@ def _direct(inp, wl, ws, nbytes):
     return st, out, args
 
 
-@pytest.mark.parametrize("name", ["t2i_512", "edit_768"])
+@pytest.mark.parametrize("name", ["t2i_512_b2", "edit_768"])
 def test_workspace_control_words_return_to_zero(name):
     """Only the control words must start at zero: the slots may hold anything.  Every
     launch leaves the control words zero again, so the next launch reuses the buffer."""
@@ -220,6 +247,7 @@ def test_workspace_control_words_return_to_zero(name):
     _, _, args = _direct(inp, wl, None, 0)
     n = _ws_bytes(args)
     nmb = -(-wl.SQ // 128)
+    assert n > 0
     ctl = _ctl_bytes(_plan(wl.B * wl.H * nmb, nmb)[0])
     g = torch.Generator(device=DEV).manual_seed(15)
     ws = torch.randint(0, 256, (n,), generator=g, device=DEV, dtype=torch.int32).to(torch.uint8)
@@ -238,8 +266,8 @@ def test_one_workspace_across_shapes():
     equals a launch on a fresh workspace.  The control words sit in a fixed region,
     so one shape's slot data never lands where the next keeps its counters."""
     _flush("case split workspace across shapes")
-    cases = [_prefill("tiny", seed=20), _prefill("t2i_512", seed=21), _prefill("multiref_cfg", seed=22),
-             _prefill("t2i_512", seed=23), _prefill("tiny", seed=24), _prefill("t2i_512", seed=25)]
+    cases = [_prefill("tiny", seed=20), _prefill("t2i_512_b2", seed=21), _prefill("multiref_cfg", seed=22),
+             _prefill("t2i_512_b2", seed=23), _prefill("tiny", seed=24), _prefill("t2i_512", seed=25)]
     sizes = [_ws_bytes(_direct(inp, wl, None, 0)[2]) for wl, inp in cases]
     shared = torch.zeros(max(sizes), dtype=torch.uint8, device=DEV)
     for (wl, inp), n in zip(cases, sizes):
@@ -253,7 +281,7 @@ def test_one_workspace_across_shapes():
 
 
 def test_workspace_checks_are_host_side():
-    wl, inp = _prefill("t2i_512", seed=16)
+    wl, inp = _prefill("t2i_512_b2", seed=16)
     _, _, args = _direct(inp, wl, None, 0)
     n = _ws_bytes(args)
     ws = torch.zeros(n + 512, dtype=torch.uint8, device=DEV)
@@ -264,11 +292,12 @@ def test_workspace_checks_are_host_side():
     torch.cuda.synchronize()
 
 
-def test_split_under_graph_replay():
+@pytest.mark.parametrize("name", ["t2i_512", "t2i_512_b2"])
+def test_split_under_graph_replay(name):
     """Captured once, replayed several times with eager launches (on the cached
     workspace) between replays: every replay equals the eager result."""
-    _flush("case split graph")
-    wl, inp = _prefill("t2i_512", seed=17)
+    _flush(f"case split graph {name}")
+    wl, inp = _prefill(name, seed=17)
     want = _run(wl, inp, True)
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
