@@ -219,6 +219,7 @@ __device__ __forceinline__ u32x4 gload16(const char* p) {
 __device__ __forceinline__ int gload_i32(const int32_t* p) { return *(const __attribute__((address_space(1))) int32_t*)p; }
 __device__ __forceinline__ float gload_f32(const float* p) { return *(const __attribute__((address_space(1))) float*)p; }
 __device__ __forceinline__ void gstore8(char* p, u32x2 v) { *(__attribute__((address_space(1))) u32x2*)p = v; }
+__device__ __forceinline__ void gstore16(char* p, u32x4 v) { *(__attribute__((address_space(1))) u32x4*)p = v; }
 __device__ __forceinline__ unsigned g_fetch_add(unsigned* p, unsigned v) {
   return __hip_atomic_fetch_add((gu32*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -227,6 +228,24 @@ __device__ __forceinline__ unsigned g_load(unsigned* p) {
 }
 __device__ __forceinline__ void g_store(unsigned* p, unsigned v) {
   __hip_atomic_store((gu32*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Barrier of one group of 4 waves of the two-group kernel (s_barrier would
+// hold both groups): an arrival counter in LDS that only grows, the group's
+// k-th barrier waiting for 4k arrivals.  The caller has waited for its tile
+// copies; the release fence waits for its LDS writes.  The spin is bounded
+// (2^22 polls of at least 64 cycles, seconds beyond any real wait), so no
+// mistake can hold the device.
+__device__ __forceinline__ void group_sync(int* ctr, int& target, int lane) {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  if (lane == 0) __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  target += 4;
+  for (int i = 0; i < (1 << 22); ++i) {
+    const int seen = __builtin_amdgcn_readfirstlane(__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+    if (seen >= target) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
 // Wave-wide min or max of an int, returned as a wave-uniform value: four DPP
@@ -332,6 +351,7 @@ __global__ void __launch_bounds__(NTHREADS * KSPLIT, KSPLIT == 1 ? 2 : 1) attn_f
   __shared__ int sred[KSPLIT][NWAVES];
   __shared__ int snext;                         // queue position handed out to this workgroup
   __shared__ f32x2 sml[KSPLIT == 2 ? NTHREADS : 1];  // group 1's (m, l) at the merge
+  __shared__ int gctr[KSPLIT];                  // group barrier arrivals (two-group kernel)
 
   // wave-uniform values go through readfirstlane so that the compiler keeps
   // them (and the buffer resources built from them) in SGPRs
@@ -342,6 +362,17 @@ __global__ void __launch_bounds__(NTHREADS * KSPLIT, KSPLIT == 1 ? 2 : 1) attn_f
   const int tid = (int)threadIdx.x & (NTHREADS - 1);  // thread of the group
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  if (KSPLIT == 2 && tid == 0) gctr[grp] = 0;  // read only after the first full barrier
+  int gtarget = 0;
+  // the barrier between tiles: the workgroup's, or the group's own in the
+  // two-group kernel (the groups then run free, as two workgroups would)
+  auto tile_sync = [&]() {
+    if constexpr (KSPLIT == 1) {
+      __syncthreads();
+    } else {
+      group_sync(&gctr[grp], gtarget, lane);
+    }
+  };
   const int hf = lane >> 5;   // lane half: keys 4*hf.. of each 8-key group
   const int l32 = lane & 31;
 
@@ -513,7 +544,10 @@ __global__ void __launch_bounds__(NTHREADS * KSPLIT, KSPLIT == 1 ? 2 : 1) attn_f
       // pieces (T, and so the split, is the same for both pieces of the item);
       // a second group with nothing to do gets an empty range
       const bool split = wk.group >= 0 && T >= SPLIT_MIN_TILES;
-      const int gsplit = (KSPLIT == 2 || p.plan.even) ? (T + 1) / 2 : (7 * T + 5) / 10;
+      // two-group kernel: group 0's waves are the older ones on every SIMD and
+      // win issue arbitration (measured: 9 tiles in 13.4 us against group 1's
+      // 17.0 us), so group 0 takes 9/16 of the tiles
+      const int gsplit = KSPLIT == 2 ? (9 * T + 8) / 16 : p.plan.even ? (T + 1) / 2 : (7 * T + 5) / 10;
       g0 = (split && wk.piece) ? gsplit : 0;
       g1 = (split && !wk.piece) ? gsplit : T;
       if (KSPLIT == 2 && !split && wk.piece) g0 = T;
@@ -719,40 +753,19 @@ __global__ void __launch_bounds__(NTHREADS * KSPLIT, KSPLIT == 1 ? 2 : 1) attn_f
     wait_copies();
     __syncthreads();
 
-    if constexpr (KSPLIT == 1) {
-      for (int g = g0; g < g1; g += 2) {
-        // tiles g0, g0 + 2, ... from stage 0, the others from stage 1 (constant LDS offsets)
-        if (g + 1 < g1) issue_tile(g + 1, 1);
-        compute_tile(g, 0);
-        if (g + 1 < g1) finish_tile(g + 1, 1);
+    for (int g = g0; g < g1; g += 2) {
+      // tiles g0, g0 + 2, ... from stage 0, the others from stage 1 (constant LDS offsets)
+      if (g + 1 < g1) issue_tile(g + 1, 1);
+      compute_tile(g, 0);
+      if (g + 1 < g1) finish_tile(g + 1, 1);
+      wait_copies();
+      tile_sync();
+      if (g + 1 < g1) {
+        if (g + 2 < g1) issue_tile(g + 2, 0);
+        compute_tile(g + 1, 1);
+        if (g + 2 < g1) finish_tile(g + 2, 0);
         wait_copies();
-        __syncthreads();
-        if (g + 1 < g1) {
-          if (g + 2 < g1) issue_tile(g + 2, 0);
-          compute_tile(g + 1, 1);
-          if (g + 2 < g1) finish_tile(g + 2, 0);
-          wait_copies();
-          __syncthreads();
-        }
-      }
-    } else {
-      // both groups step through group 0's tile count (group 1 has at most as
-      // many) so that they reach every barrier together
-      const int nsteps = split ? (T + 1) / 2 : T;
-      for (int st = 0; st < nsteps; st += 2) {
-        const int g = g0 + st;
-        if (g + 1 < g1) issue_tile(g + 1, 1);
-        if (g < g1) compute_tile(g, 0);
-        if (g + 1 < g1) finish_tile(g + 1, 1);
-        wait_copies();
-        __syncthreads();
-        if (st + 1 < nsteps) {
-          if (g + 2 < g1) issue_tile(g + 2, 0);
-          if (g + 1 < g1) compute_tile(g + 1, 1);
-          if (g + 2 < g1) finish_tile(g + 2, 0);
-          wait_copies();
-          __syncthreads();
-        }
+        tile_sync();
       }
     }
 
@@ -882,22 +895,65 @@ __global__ void __launch_bounds__(NTHREADS * KSPLIT, KSPLIT == 1 ? 2 : 1) attn_f
         }
     }
 
-    // ---- epilogue: out = l > 0 ? acc / l : 0 (triton_attention.py:166-168)
+    // ---- epilogue: out = l > 0 ? acc / l : 0 (triton_attention.py:166-168).
+    // A lane holds half of one row's D values; the wave's 32 rows go out
+    // through its own 32 x ROWB bytes of LDS (in K stages 0-1: free after the
+    // tile loop's last barrier, and written by the next unit's copies only
+    // behind the draw's barriers), read back as whole rows, so that a store
+    // instruction writes 1 KiB of whole rows instead of 16 B into each of 32
+    // rows (which took ~2 us per unit, measured).  Rows past SQ are not stored.
     const float l_tot = pair_sum(l_part);
     const float inv = (l_tot > 0.0f) ? 1.0f / l_tot : 0.0f;
     if (pulled && tid == 0) snext = gx + (int)pend;
-    if (live && grp == 0) {
-      char* orow = pe.out + (b * pe.so[0] + (int64_t)m * pe.so[1] + h * pe.so[2]) * 2;
+    if constexpr (V_FP8 || KV) {
+      // kernels that write LDS inside the tile loop (the fp8 V dequantisation,
+      // the key_valid bytes) store straight from the registers: with the LDS
+      // staging below the compiler serialises their PV block's LDS reads
+      // (48-64 full waits in the tile loop instead of 18-34)
+      if (live && grp == 0) {
+        char* orow = pe.out + (b * pe.so[0] + (int64_t)m * pe.so[1] + h * pe.so[2]) * 2;
 #pragma unroll
-      for (int db = 0; db < DBLK; ++db)
+        for (int db = 0; db < DBLK; ++db)
 #pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-          const int d = db * 32 + 8 * q4 + 4 * hf;
-          u32x2 w;
-          w.x = pack2<FP16>(oacc[db][4 * q4 + 0] * inv, oacc[db][4 * q4 + 1] * inv);
-          w.y = pack2<FP16>(oacc[db][4 * q4 + 2] * inv, oacc[db][4 * q4 + 3] * inv);
-          gstore8(orow + d * 2, w);
+          for (int q4 = 0; q4 < 4; ++q4) {
+            const int d = db * 32 + 8 * q4 + 4 * hf;
+            u32x2 w;
+            w.x = pack2<FP16>(oacc[db][4 * q4 + 0] * inv, oacc[db][4 * q4 + 1] * inv);
+            w.y = pack2<FP16>(oacc[db][4 * q4 + 2] * inv, oacc[db][4 * q4 + 3] * inv);
+            gstore8(orow + d * 2, w);
+          }
+      }
+    } else {
+      if (grp == 0) {
+        // the lane index goes through an empty asm here: the offsets below are the
+        // same for every unit, and hoisted out of the unit loop they would hold
+        // ~24 registers through the tile loop
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        const int r32 = ln & 31, half = ln >> 5;
+        char* const ow = kst[0] + wave * (32 * ROWB);
+#pragma unroll
+        for (int db = 0; db < DBLK; ++db)
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4) {
+            // 16-byte chunk c of row r32 holds d = 8c .. 8c + 7; this lane's four are 4half ..
+            const int c = db * 4 + q4;
+            u32x2 w;
+            w.x = pack2<FP16>(oacc[db][4 * q4 + 0] * inv, oacc[db][4 * q4 + 1] * inv);
+            w.y = pack2<FP16>(oacc[db][4 * q4 + 2] * inv, oacc[db][4 * q4 + 3] * inv);
+            *reinterpret_cast<u32x2*>(ow + r32 * ROWB + ((c ^ swz<CH>(r32)) << 4) + 8 * half) = w;
+          }
+        constexpr int RPI = 64 / CH;  // rows per store instruction
+        const int rr = ln / CH, cc = ln % CH;
+        const int row0 = mb * BM + wave * 32;
+        char* const obase = pe.out + (b * pe.so[0] + h * pe.so[2]) * 2;
+#pragma unroll
+        for (int i = 0; i < 32 / RPI; ++i) {
+          const int r = i * RPI + rr;
+          const u32x4 v = lds128(ow + r * ROWB + ((cc ^ swz<CH>(r)) << 4));
+          if (row0 + r < pe.SQ) gstore16(obase + (int64_t)(row0 + r) * pe.so[1] * 2 + cc * 16, v);
         }
+      }
     }
   }  // units
 
