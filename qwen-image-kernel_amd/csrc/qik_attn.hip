@@ -234,13 +234,13 @@ __device__ __forceinline__ void g_store(unsigned* p, unsigned v) {
 // hold both groups): an arrival counter in LDS that only grows, the group's
 // k-th barrier waiting for 4k arrivals.  The caller has waited for its tile
 // copies; the release fence waits for its LDS writes.  The spin is bounded
-// (2^22 polls of at least 64 cycles, seconds beyond any real wait), so no
+// (2^18 polls of at least 64 cycles, milliseconds beyond any real wait), so no
 // mistake can hold the device.
 __device__ __forceinline__ void group_sync(int* ctr, int& target, int lane) {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   if (lane == 0) __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   target += 4;
-  for (int i = 0; i < (1 << 22); ++i) {
+  for (int i = 0; i < (1 << 18); ++i) {
     const int seen = __builtin_amdgcn_readfirstlane(__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
     if (seen >= target) break;
     __builtin_amdgcn_s_sleep(1);
