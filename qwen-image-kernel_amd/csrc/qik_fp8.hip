@@ -308,18 +308,25 @@ __global__ void __launch_bounds__(QT) dequant_kernel(const unsigned char* w, con
 constexpr int GT = 256;  // threads per GEMM workgroup (4 waves)
 constexpr int KB = 64;   // k bytes per stage (one MFMA k-step)
 
+// A range of output columns computed with one tile shape.
+struct GemmRegion {
+  const unsigned char* w;  // weight row of the region's first column
+  const char* bias;        // its first bias element, or null
+  char* out;               // its first output column
+  int N;                   // columns in the region
+  int ntm, ntn;            // tiles along m and n
+  int group_m;             // tile rows per group of the tile order
+  int wgs;                 // workgroups: tiles rounded up to a multiple of 8
+};
+
 struct GemmParams {
   const unsigned char* a;
-  const unsigned char* w;
   const float* sa;
   const float* sw;
-  const char* bias;
-  char* out;
-  int M, N, K;
+  int M, K;
   int lda, ldw;   // bytes
   int64_t ldc;    // elements
-  int ntm, ntn;   // tiles along m and n
-  int group_m;    // tile rows per group of the tile order
+  GemmRegion r[2];  // columns [0, n1) with the larger tile, then [n1, N)
 };
 
 template <int BM_, int BN_, int NS_>
@@ -371,32 +378,33 @@ __device__ __forceinline__ void wait_vmcnt() {
 // contiguous KiB.
 __device__ __forceinline__ int swz(int r) { return (r >> 2) & 3; }
 
+// One BM x BN output tile of region g; bx counts the region's workgroups
+// (bx % 8 is the XCD: every region starts at a multiple of 8).
 template <class C, bool FP16>
-__global__ void __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(1, 1)))
-fp8_gemm_kernel(const GemmParams p) {
-  __shared__ __attribute__((aligned(1024))) unsigned char lds[C::NS * C::STAGE];
+__device__ __forceinline__ void gemm_tile(const GemmParams& p, const GemmRegion& rg, const int bx,
+                                          unsigned char* lds) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: copy targets go to SGPRs
   const int wm = wave & 1, wn = wave >> 1;
 
-  // tile of this workgroup: XCD x = blockIdx % 8 takes a contiguous run of
-  // the tile order, which walks group_m tile rows at a time
-  const int T = p.ntm * p.ntn;
-  const int bx = blockIdx.x;
+  // tile of this workgroup: XCD x takes a contiguous run of the tile order,
+  // which walks group_m tile rows at a time; the padding workgroups leave
+  const int T = rg.ntm * rg.ntn;
   const int x = bx & 7, s = bx >> 3;
   const int q = T >> 3, r = T & 7;
+  if (s >= q + (x < r ? 1 : 0)) return;
   const int t = x * q + min(x, r) + s;
-  const int gsz_full = p.group_m * p.ntn;
+  const int gsz_full = rg.group_m * rg.ntn;
   const int g = t / gsz_full;
-  const int first = g * p.group_m;
-  const int gm = min(p.group_m, p.ntm - first);
+  const int first = g * rg.group_m;
+  const int gm = min(rg.group_m, rg.ntm - first);
   const int tr = t - g * gsz_full;
   const int tm = first + tr % gm;
   const int tn = tr / gm;
   const int m0 = tm * C::BM, n0 = tn * C::BN;
   const int mrows = min(C::BM, p.M - m0);
-  const int nrows = min(C::BN, p.N - n0);
+  const int nrows = min(C::BN, rg.N - n0);
 
   // per-lane copy offsets: copy i of this wave fills 16-row group wave + 4 i
   // of its tile; lane l writes row l/4 of the group, physical chunk l%4,
@@ -410,7 +418,7 @@ fp8_gemm_kernel(const GemmParams p) {
   for (int i = 0; i < C::WI; ++i) woff[i] = (uint32_t)((crow + 64 * i) * p.ldw + cchunk);
   const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_ptr_t)lds;
   const unsigned char* abase = p.a + (int64_t)m0 * p.lda;
-  const unsigned char* wbase = p.w + (int64_t)n0 * p.ldw;
+  const unsigned char* wbase = rg.w + (int64_t)n0 * p.ldw;
   const int nk = (p.K + KB - 1) / KB;
 
   // copy state of one k-step: the stage's LDS address and the two buffer
@@ -518,7 +526,18 @@ fp8_gemm_kernel(const GemmParams p) {
   }
   if (kt < nk) step(kt, 0);
 
-  // epilogue: out[m][n..n+3] = round(acc * (sa * sw) + bias[n..n+3])
+  // epilogue: out[m][n..n+3] = round(acc * (sa * sw) + bias[n..n+3]),
+  // staged through LDS: a lane's results are 4 columns of one row, so stored
+  // straight from the accumulators every store instruction would touch 32
+  // rows; from LDS each one writes whole rows of the tile (64 lanes x 16 B).
+  // Staged row ml keeps its 16-byte chunk c at physical chunk c ^ (ml % CPR),
+  // which spreads a fragment's 32 rows over the banks.
+  constexpr int RB = C::BN * 2;   // bytes of a staged row
+  constexpr int CPR = RB / 16;    // 16-byte chunks per row
+  constexpr int RPI = 64 / CPR;   // rows per store instruction
+  static_assert(C::BM * RB <= C::NS * C::STAGE, "the output tile fits the stages");
+  wait_vmcnt<0>();  // the copies of the steps past the end still land in their stages
+  __syncthreads();  // and every wave is done with the last stage's fragments
   {
 #pragma clang fp contract(off)
     const float ab = p.sa[0] * p.sw[0];
@@ -526,18 +545,17 @@ fp8_gemm_kernel(const GemmParams p) {
     for (int j = 0; j < C::NJ; ++j) {
 #pragma unroll
       for (int qd = 0; qd < 4; ++qd) {
-        const int n = n0 + wn * C::WN + j * 32 + qd * 8 + (lane >> 5) * 4;
-        if (n >= p.N) continue;
+        const int nl = wn * C::WN + j * 32 + qd * 8 + (lane >> 5) * 4;
+        const int n = n0 + nl;
         float bv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (p.bias != nullptr) {
-          const u32x2 braw = *reinterpret_cast<const u32x2*>(p.bias + (int64_t)n * 2);
+        if (rg.bias != nullptr && n < rg.N) {
+          const u32x2 braw = *reinterpret_cast<const u32x2*>(rg.bias + (int64_t)n * 2);
           unpack2<FP16>(braw.x, bv[0], bv[1]);
           unpack2<FP16>(braw.y, bv[2], bv[3]);
         }
 #pragma unroll
         for (int i = 0; i < C::MI; ++i) {
-          const int m = m0 + wm * C::WM + i * 32 + (lane & 31);
-          if (m >= p.M) continue;
+          const int ml = wm * C::WM + i * 32 + (lane & 31);
           float y[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
@@ -545,11 +563,36 @@ fp8_gemm_kernel(const GemmParams p) {
             y[e] = y[e] + bv[e];
           }
           const u32x2 o = {pack2<FP16>(y[0], y[1]), pack2<FP16>(y[2], y[3])};
-          *reinterpret_cast<u32x2*>(p.out + (m * p.ldc + n) * 2) = o;
+          const int phys = (nl >> 3) ^ (ml & (CPR - 1));
+          *reinterpret_cast<u32x2*>(lds + ml * RB + phys * 16 + (lane >> 5) * 8) = o;
         }
       }
     }
   }
+  __syncthreads();
+  const int c = lane % CPR;
+  const int n = n0 + c * 8;
+#pragma unroll 4
+  for (int r0 = wave * RPI; r0 < C::BM; r0 += 4 * RPI) {
+    const int ml = r0 + lane / CPR;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(lds + ml * RB + ((c ^ (ml & (CPR - 1))) * 16));
+    const int m = m0 + ml;
+    if (m < p.M && n < rg.N) *reinterpret_cast<u32x4*>(rg.out + ((int64_t)m * p.ldc + n) * 2) = v;
+  }
+}
+
+// Workgroups [0, r[0].wgs) compute region 0 with C1 tiles, the rest region 1
+// with C2 tiles.  The dispatcher starts workgroups in index order, so the
+// smaller tiles of region 1 fill the CUs that the last round of region 0
+// leaves free.
+template <class C1, class C2, bool FP16>
+__global__ void __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(1, 1)))
+fp8_gemm_kernel(const GemmParams p) {
+  constexpr int LDS1 = C1::NS * C1::STAGE, LDS2 = C2::NS * C2::STAGE;
+  __shared__ __attribute__((aligned(1024))) unsigned char lds[LDS1 > LDS2 ? LDS1 : LDS2];
+  const int bx = blockIdx.x;
+  if (bx < p.r[0].wgs) gemm_tile<C1, FP16>(p, p.r[0], bx, lds);
+  else gemm_tile<C2, FP16>(p, p.r[1], bx - p.r[0].wgs, lds);
 }
 
 }  // namespace qik_fp8
@@ -607,30 +650,75 @@ typedef Cfg<256, 256, 4> Cfg256x256;
 typedef Cfg<256, 128, 4> Cfg256x128;
 typedef Cfg<128, 128, 4> Cfg128x128;
 
-struct TileChoice {
+// Time of a tile of each shape relative to a 256 x 256 tile: area / rate,
+// the rates measured on MI355X with each shape forced over whole launches
+// (1536x4096x4096 50.0 / 35.1 / 45.8 us, 4352x9216x3072 146.7 / 153.1 /
+// 201.1 us, 4352x3072x12288 141.4 / 188.0 / 265.1 us for 256x256 / 256x128 /
+// 128x128).  A 256 x 128 tile moves 24 KiB into LDS per 512 MFMA cycles,
+// close to what the copy path sustains, so it runs at about 0.8 of the big
+// tile's rate per output, and 128 x 128 at about 0.6.
+struct TileShape {
   int bm, bn;
+  double t;
+};
+static const TileShape kShapes[3] = {{256, 256, 1.0}, {256, 128, 0.5 / 0.8}, {128, 128, 0.25 / 0.6}};
+
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Finish time of one XCD whose P CUs run t1 tiles of time d1 and then t2
+// tiles of time d2, one workgroup per CU (a 256-thread workgroup of these
+// tiles holds a CU's four SIMDs), each started on the CU that frees first.
+double xcd_makespan(int64_t t1, double d1, int64_t t2, double d2, int64_t P) {
+  const int64_t full = t1 / P, rem = t1 % P;
+  const double a = (double)full * d1, b = a + d1;  // CUs free after t1: P - rem at a, rem at b
+  const int64_t na = P - rem, nb = rem;
+  const double end1 = nb > 0 ? b : a;
+  if (t2 == 0) return end1;
+  // the j-th tile of t2 starts at the j-th smallest of {a + k d2} (na times
+  // each) and {b + k d2} (nb times each)
+  int64_t ka = 0, kb = 0, placed = 0;
+  double last = a;
+  while (placed < t2) {
+    const double ta = a + (double)ka * d2, tb = nb > 0 ? b + (double)kb * d2 : 1e300;
+    if (ta <= tb) {
+      last = ta;
+      placed += na;
+      ++ka;
+    } else {
+      last = tb;
+      placed += nb;
+      ++kb;
+    }
+  }
+  return std::max(end1, last + d2);
+}
+
+// Columns [0, n1) with tile shape `big`, [n1, N) with shape big + 1.
+struct GemmPlan {
+  int big;
+  int64_t n1;
 };
 
-// The tile shape with the shortest estimated makespan on `cus` CUs: a CU's
-// workgroups share its matrix cores, so the makespan is about
-// ceil(tiles / cus) tiles of work per CU, each at the shape's measured rate
-// relative to the 256 x 256 tile.
-TileChoice choose_tile(int64_t M, int64_t N, int cus) {
-  struct Cand {
-    int bm, bn;
-    double rel_rate;
-  };
-  static const Cand cands[] = {{256, 256, 1.0}, {256, 128, 0.9}, {128, 128, 0.75}};
-  if (cus <= 0) cus = 256;
-  TileChoice best = {256, 256};
-  double best_cost = 1e300;
-  for (const Cand& c : cands) {
-    const int64_t tiles = ((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn);
-    const int64_t rounds = (tiles + cus - 1) / cus;
-    const double cost = (double)rounds * c.bm * c.bn / c.rel_rate;
-    if (cost < best_cost * 0.999) {
-      best_cost = cost;
-      best = {c.bm, c.bn};
+// The split with the shortest estimated makespan on `cus` CUs.  Workgroups go
+// to the XCDs in turn, so the XCD that finishes last holds ceil(tiles / 8) of
+// each region.  The split points are whole big-tile columns; n1 = N is one
+// region of the big shape, n1 = 0 one of the next shape.
+GemmPlan choose_plan(int64_t M, int64_t N, int cus) {
+  const int64_t P = std::max(1, (cus > 0 ? cus : 256) / 8);
+  GemmPlan best = {0, N};
+  double best_t = 1e300;
+  for (int big = 0; big < 2; ++big) {
+    const TileShape& s1 = kShapes[big];
+    const TileShape& s2 = kShapes[big + 1];
+    for (int64_t k = cdiv(N, s1.bn); k >= 0; --k) {
+      const int64_t n1 = std::min(k * s1.bn, N);
+      const int64_t t1 = cdiv(M, s1.bm) * cdiv(n1, s1.bn);
+      const int64_t t2 = cdiv(M, s2.bm) * cdiv(N - n1, s2.bn);
+      const double t = xcd_makespan(cdiv(t1, 8), s1.t, cdiv(t2, 8), s2.t, P);
+      if (t < best_t * 0.999) {
+        best_t = t;
+        best = {big, n1};
+      }
     }
   }
   return best;
@@ -655,16 +743,31 @@ int choose_group_m(int ntm, int ntn, int bm, int bn) {
   return best;
 }
 
+// Region of columns [c0, c1) of the call with tile shape C.
 template <class C>
-int launch_gemm(GemmParams p, bool fp16, hipStream_t s) {
-  p.ntm = (p.M + C::BM - 1) / C::BM;
-  p.ntn = (p.N + C::BN - 1) / C::BN;
-  p.group_m = choose_group_m(p.ntm, p.ntn, C::BM, C::BN);
-  const int64_t tiles = (int64_t)p.ntm * p.ntn;
-  if (tiles > (int64_t)INT_MAX) return QIK_ERR_SHAPE;
+int set_region(GemmRegion& rg, const qik_fp8_gemm_args* a, int64_t c0, int64_t c1) {
+  rg.w = static_cast<const unsigned char*>(a->w) + c0 * a->ldw;
+  rg.bias = a->bias != nullptr ? static_cast<const char*>(a->bias) + c0 * 2 : nullptr;
+  rg.out = static_cast<char*>(a->out) + c0 * 2;
+  rg.N = (int)(c1 - c0);
+  rg.ntm = (int)cdiv(a->M, C::BM);
+  rg.ntn = (int)cdiv(c1 - c0, C::BN);
+  rg.group_m = choose_group_m(rg.ntm, rg.ntn, C::BM, C::BN);
+  const int64_t wgs = cdiv((int64_t)rg.ntm * rg.ntn, 8) * 8;
+  if (wgs > (int64_t)INT_MAX / 2) return QIK_ERR_SHAPE;
+  rg.wgs = (int)wgs;
+  return QIK_OK;
+}
+
+template <class C1, class C2>
+int launch_gemm(GemmParams& p, const qik_fp8_gemm_args* a, int64_t n1, bool fp16, hipStream_t s) {
+  int st = set_region<C1>(p.r[0], a, 0, n1);
+  if (st == QIK_OK) st = set_region<C2>(p.r[1], a, n1, a->N);
+  if (st != QIK_OK) return st;
+  const unsigned grid = (unsigned)p.r[0].wgs + (unsigned)p.r[1].wgs;
   void* args[] = {&p};
-  const void* fn = fp16 ? (const void*)fp8_gemm_kernel<C, true> : (const void*)fp8_gemm_kernel<C, false>;
-  return hipLaunchKernel(fn, dim3((unsigned)tiles), dim3(GT), args, 0, s) == hipSuccess ? QIK_OK : QIK_ERR_LAUNCH;
+  const void* fn = fp16 ? (const void*)fp8_gemm_kernel<C1, C2, true> : (const void*)fp8_gemm_kernel<C1, C2, false>;
+  return hipLaunchKernel(fn, dim3(grid), dim3(GT), args, 0, s) == hipSuccess ? QIK_OK : QIK_ERR_LAUNCH;
 }
 
 }  // namespace qik_fp8
@@ -722,23 +825,18 @@ int qik_fp8_gemm(const qik_fp8_gemm_args* a, void* stream) {
   GemmParams p;
   memset(&p, 0, sizeof(p));
   p.a = static_cast<const unsigned char*>(a->a);
-  p.w = static_cast<const unsigned char*>(a->w);
   p.sa = a->scale_a;
   p.sw = a->scale_w;
-  p.bias = static_cast<const char*>(a->bias);
-  p.out = static_cast<char*>(a->out);
   p.M = (int)a->M;
-  p.N = (int)a->N;
   p.K = (int)a->K;
   p.lda = (int)a->lda;
   p.ldw = (int)a->ldw;
   p.ldc = a->ldc;
   const bool fp16 = a->out_dtype == QIK_DTYPE_FP16;
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  const TileChoice tc = choose_tile(a->M, a->N, device_cus());
-  if (tc.bm == 256 && tc.bn == 256) return launch_gemm<Cfg256x256>(p, fp16, s);
-  if (tc.bm == 256) return launch_gemm<Cfg256x128>(p, fp16, s);
-  return launch_gemm<Cfg128x128>(p, fp16, s);
+  const GemmPlan plan = choose_plan(a->M, a->N, device_cus());
+  if (plan.big == 0) return launch_gemm<Cfg256x256, Cfg256x128>(p, a, plan.n1, fp16, s);
+  return launch_gemm<Cfg256x128, Cfg128x128>(p, a, plan.n1, fp16, s);
 }
 
 int qik_fp8_dequant(const void* w, const float* scale, void* out, int64_t n, int32_t out_dtype, void* stream) {
