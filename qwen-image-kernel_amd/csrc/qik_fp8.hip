@@ -305,7 +305,6 @@ __global__ void __launch_bounds__(QT) dequant_kernel(const unsigned char* w, con
 // GEMM
 // ---------------------------------------------------------------------------
 
-constexpr int GT = 256;  // threads per GEMM workgroup (4 waves)
 constexpr int KB = 64;   // k bytes per stage (one MFMA k-step)
 
 // A range of output columns computed with one tile shape.
@@ -329,17 +328,21 @@ struct GemmParams {
   GemmRegion r[2];  // columns [0, n1) with the larger tile, then [n1, N)
 };
 
-template <int BM_, int BN_, int NS_>
+template <int BM_, int BN_, int NS_, int WGM_ = 2, int WGN_ = 2>
 struct Cfg {
   static constexpr int BM = BM_, BN = BN_, NS = NS_;
-  static constexpr int WM = BM / 2, WN = BN / 2;  // wave tile (2 x 2 waves)
+  static constexpr int WGM = WGM_, WGN = WGN_;     // waves along m and n
+  static constexpr int NW = WGM * WGN, NT = 64 * NW;
+  static constexpr int WM = BM / WGM, WN = BN / WGN;  // wave tile
   static constexpr int MI = WM / 32, NJ = WN / 32;
   static constexpr int A_BYTES = BM * KB;          // A tile of one stage
   static constexpr int STAGE = (BM + BN) * KB;
-  static constexpr int AI = BM / 64;               // 1 KiB copies of A per wave per stage
-  static constexpr int WI = BN / 64;
+  static constexpr int AI = BM / (16 * NW);        // 1 KiB copies of A per wave per stage
+  static constexpr int WI = BN / (16 * NW);
   static constexpr int COPIES = AI + WI;
-  static_assert(BM % 64 == 0 && BN % 64 == 0, "tiles are multiples of 64");
+  static_assert(NW == 4 || NW == 8, "one or two waves per SIMD");
+  static_assert(AI * 16 * NW == BM && WI * 16 * NW == BN, "whole copies per wave");
+  static_assert(MI * 32 == WM && NJ * 32 == WN, "whole MFMA blocks per wave");
   static_assert(NS >= 3, "copies run at least two stages ahead");
 };
 
@@ -386,7 +389,7 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, const GemmRegion&
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: copy targets go to SGPRs
-  const int wm = wave & 1, wn = wave >> 1;
+  const int wm = wave % C::WGM, wn = wave / C::WGM;
 
   // tile of this workgroup: XCD x takes a contiguous run of the tile order,
   // which walks group_m tile rows at a time; the padding workgroups leave
@@ -406,16 +409,16 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, const GemmRegion&
   const int mrows = min(C::BM, p.M - m0);
   const int nrows = min(C::BN, rg.N - n0);
 
-  // per-lane copy offsets: copy i of this wave fills 16-row group wave + 4 i
+  // per-lane copy offsets: copy i of this wave fills 16-row group wave + NW i
   // of its tile; lane l writes row l/4 of the group, physical chunk l%4,
   // which holds logical chunk (l%4) ^ swz(row)
   const int crow = wave * 16 + (lane >> 2);
   const int cchunk = ((lane & 3) ^ ((lane >> 4) & 3)) * 16;
   uint32_t aoff[C::AI], woff[C::WI];
 #pragma unroll
-  for (int i = 0; i < C::AI; ++i) aoff[i] = (uint32_t)((crow + 64 * i) * p.lda + cchunk);
+  for (int i = 0; i < C::AI; ++i) aoff[i] = (uint32_t)((crow + 16 * C::NW * i) * p.lda + cchunk);
 #pragma unroll
-  for (int i = 0; i < C::WI; ++i) woff[i] = (uint32_t)((crow + 64 * i) * p.ldw + cchunk);
+  for (int i = 0; i < C::WI; ++i) woff[i] = (uint32_t)((crow + 16 * C::NW * i) * p.ldw + cchunk);
   const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_ptr_t)lds;
   const unsigned char* abase = p.a + (int64_t)m0 * p.lda;
   const unsigned char* wbase = rg.w + (int64_t)n0 * p.ldw;
@@ -445,8 +448,8 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, const GemmRegion&
   };
   // copy i of this wave's list (A copies first, then W)
   auto issue = [&](const StepCopies& sc, const int i) __attribute__((always_inline)) {
-    if (i < C::AI) dma16(sc.ra, sc.st + (uint32_t)((wave + 4 * i) * 1024), aoff[i] | sc.dead);
-    else dma16(sc.rw, sc.st + (uint32_t)(C::A_BYTES + (wave + 4 * (i - C::AI)) * 1024), woff[i - C::AI] | sc.dead);
+    if (i < C::AI) dma16(sc.ra, sc.st + (uint32_t)((wave + C::NW * i) * 1024), aoff[i] | sc.dead);
+    else dma16(sc.rw, sc.st + (uint32_t)(C::A_BYTES + (wave + C::NW * (i - C::AI)) * 1024), woff[i - C::AI] | sc.dead);
   };
   auto copy_stage = [&](const int kt) __attribute__((always_inline)) {
     const StepCopies sc = prepare(kt);
@@ -459,22 +462,26 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, const GemmRegion&
   const int frow = lane & 31;
   const uint32_t f0 = (uint32_t)(frow * KB + (((lane >> 5) * 2) ^ swz(frow)) * 16);
   const uint32_t f1 = (uint32_t)(frow * KB + (((lane >> 5) * 2 + 1) ^ swz(frow)) * 16);
-  auto read_frags = [&](const int kt, i32x8 (&fa)[C::MI], i32x8 (&fw)[C::NJ]) __attribute__((always_inline)) {
+  // half r % 2 of fragment r / 2 (A fragments first, then W) of stage kt
+  constexpr int NRD = 2 * (C::MI + C::NJ);
+  auto read_frag = [&](const int kt, const int r, i32x8 (&fa)[C::MI], i32x8 (&fw)[C::NJ])
+      __attribute__((always_inline)) {
     const unsigned char* st = lds + (kt % C::NS) * C::STAGE;
+    const int f = r >> 1;
+    const uint32_t off = (r & 1) ? f1 : f0;
+    const unsigned char* b = f < C::MI ? st + (wm * C::WM + f * 32) * KB
+                                       : st + C::A_BYTES + (wn * C::WN + (f - C::MI) * 32) * KB;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(b + off);
+    i32x8& dst = f < C::MI ? fa[f] : fw[f - C::MI];
+    const int e = (r & 1) * 4;
+    dst[e] = (int)v.x;
+    dst[e + 1] = (int)v.y;
+    dst[e + 2] = (int)v.z;
+    dst[e + 3] = (int)v.w;
+  };
+  auto read_frags = [&](const int kt, i32x8 (&fa)[C::MI], i32x8 (&fw)[C::NJ]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < C::MI; ++i) {
-      const unsigned char* b = st + (wm * C::WM + i * 32) * KB;
-      const u32x4 lo = *reinterpret_cast<const u32x4*>(b + f0);
-      const u32x4 hi = *reinterpret_cast<const u32x4*>(b + f1);
-      fa[i] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-    }
-#pragma unroll
-    for (int j = 0; j < C::NJ; ++j) {
-      const unsigned char* b = st + C::A_BYTES + (wn * C::WN + j * 32) * KB;
-      const u32x4 lo = *reinterpret_cast<const u32x4*>(b + f0);
-      const u32x4 hi = *reinterpret_cast<const u32x4*>(b + f1);
-      fw[j] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-    }
+    for (int r = 0; r < NRD; ++r) read_frag(kt, r, fa, fw);
   };
 
   f32x16 acc[C::NJ][C::MI];
@@ -492,31 +499,38 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, const GemmRegion&
   read_frags(0, fa[0], fw[0]);
 
   // k-step kt: publish stage kt+1 (its copies done, and every wave past its
-  // MFMAs of kt-1, so stage kt-1 = kt+NS-1 is free), read its fragments,
-  // then run the MFMAs of kt with the copies of kt+NS-1 between them
-  // (sched_barrier(0) pins: the compiler would otherwise hoist the wait and
-  // barrier of the next step above this step's MFMAs, exposing the copies'
-  // whole latency, and bunch the copies together)
+  // MFMAs of kt-1, so stage kt-1 = kt+NS-1 is free), then run the MFMAs of kt
+  // with the fragment reads of kt+1 between the first half of them and the
+  // copies of kt+NS-1 between the second half.  Issued as one burst, the 16
+  // reads of a 256 x 256 tile held the wave at its second MFMA while the
+  // matrix core idled.  sched_barrier(0) pins the order: the compiler would
+  // otherwise hoist the wait and barrier of the next step above this step's
+  // MFMAs and bunch the reads and copies together.  The reads of the step
+  // after the last (a stage whose contents are not used) are issued too, so
+  // the step stays one basic block.
   auto step = [&](const int kt, const int cur) __attribute__((always_inline)) {
+    constexpr int NMF = C::NJ * C::MI;
+    constexpr int H = NMF / 2;  // MFMAs with reads after them
     __builtin_amdgcn_sched_barrier(0);
     wait_vmcnt<(C::NS - 3) * C::COPIES>();
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
-    if (kt + 1 < nk) read_frags(kt + 1, fa[cur ^ 1], fw[cur ^ 1]);
-    constexpr int NMF = C::NJ * C::MI;
     const StepCopies sc = prepare(kt + C::NS - 1);
 #pragma unroll
     for (int idx = 0; idx < NMF; ++idx) {
       const int j = idx / C::MI, i = idx % C::MI;
       acc[j][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fw[cur][j], fa[cur][i], acc[j][i], 0, 0, 0, 0,
                                                                    0, 0);
-      // this wave's copies spread evenly over the MFMAs
+      __builtin_amdgcn_sched_barrier(0);
+      if (idx < H) {
 #pragma unroll
-      for (int c = idx * C::COPIES / NMF; c < (idx + 1) * C::COPIES / NMF; ++c) {
-        __builtin_amdgcn_sched_barrier(0);
-        issue(sc, c);
-        __builtin_amdgcn_sched_barrier(0);
+        for (int r = idx * NRD / H; r < (idx + 1) * NRD / H; ++r) read_frag(kt + 1, r, fa[cur ^ 1], fw[cur ^ 1]);
+      } else {
+#pragma unroll
+        for (int c = (idx - H) * C::COPIES / (NMF - H); c < (idx - H + 1) * C::COPIES / (NMF - H); ++c)
+          issue(sc, c);
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
   int kt = 0;
@@ -573,7 +587,7 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, const GemmRegion&
   const int c = lane % CPR;
   const int n = n0 + c * 8;
 #pragma unroll 4
-  for (int r0 = wave * RPI; r0 < C::BM; r0 += 4 * RPI) {
+  for (int r0 = wave * RPI; r0 < C::BM; r0 += C::NW * RPI) {
     const int ml = r0 + lane / CPR;
     const u32x4 v = *reinterpret_cast<const u32x4*>(lds + ml * RB + ((c ^ (ml & (CPR - 1))) * 16));
     const int m = m0 + ml;
@@ -586,8 +600,9 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, const GemmRegion&
 // smaller tiles of region 1 fill the CUs that the last round of region 0
 // leaves free.
 template <class C1, class C2, bool FP16>
-__global__ void __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ void __launch_bounds__(C1::NT) __attribute__((amdgpu_waves_per_eu(C1::NW / 4, C1::NW / 4)))
 fp8_gemm_kernel(const GemmParams p) {
+  static_assert(C1::NT == C2::NT, "one workgroup size per launch");
   constexpr int LDS1 = C1::NS * C1::STAGE, LDS2 = C2::NS * C2::STAGE;
   __shared__ __attribute__((aligned(1024))) unsigned char lds[LDS1 > LDS2 ? LDS1 : LDS2];
   const int bx = blockIdx.x;
@@ -767,7 +782,7 @@ int launch_gemm(GemmParams& p, const qik_fp8_gemm_args* a, int64_t n1, bool fp16
   const unsigned grid = (unsigned)p.r[0].wgs + (unsigned)p.r[1].wgs;
   void* args[] = {&p};
   const void* fn = fp16 ? (const void*)fp8_gemm_kernel<C1, C2, true> : (const void*)fp8_gemm_kernel<C1, C2, false>;
-  return hipLaunchKernel(fn, dim3(grid), dim3(GT), args, 0, s) == hipSuccess ? QIK_OK : QIK_ERR_LAUNCH;
+  return hipLaunchKernel(fn, dim3(grid), dim3(C1::NT), args, 0, s) == hipSuccess ? QIK_OK : QIK_ERR_LAUNCH;
 }
 
 }  // namespace qik_fp8
