@@ -395,18 +395,36 @@ __global__ void __launch_bounds__(QTHREADS) slab_quant_fp8_kernel(const QuantPar
     scale = p.scale[bh];
   }
   char* dst = p.dst + b * p.sd[0] + h * p.sd[1] + t * 8;
+  // v / scale rounded to nearest, as an IEEE division gives it, from the
+  // correctly rounded reciprocal y of the scale and one correction:
+  // q = RN(v*y) is within an ulp of v/scale, r = v - q*scale is exact (fma),
+  // and RN(q + r*y) is the correctly rounded quotient (Markstein's theorem,
+  // which needs no overflow or underflow on the way: every |v| is at most the
+  // amax its scale came from, so |v/scale| <= 448 (1 + 2^-22), and a quotient
+  // that is subnormal rounds to a zero code either way).  The quotient takes
+  // v's sign, which keeps -0 for v = -0.  A non-finite scale (an inf in the
+  // head) has no exact remainder; the division is kept there.
+  const float rcp = 1.0f / scale;
+  const bool fast = __builtin_isfinite(scale);
+  auto quot = [&](const float x) __attribute__((always_inline)) {
+    if (!fast) return x / scale;
+    const float q = x * rcp;
+    const float r = __builtin_fmaf(-q, scale, x);
+    return __builtin_copysignf(__builtin_fmaf(r, rcp, q), x);
+  };
   for (;;) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (q0 + u * RPS >= p1) continue;
       const unsigned w[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
-      // v / scale (IEEE division), clamped to the e4m3fn range, rounded to
-      // nearest even by the hardware conversion; byte k of the 8 = element 8t+k
+      // v / scale (correctly rounded, above), clamped to the e4m3fn range,
+      // rounded to nearest even by the hardware conversion; byte k of the 8 =
+      // element 8t+k
       float q[8];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        q[2 * i] = fminf(fmaxf(__uint_as_float(w[i] << 16) / scale, -448.0f), 448.0f);
-        q[2 * i + 1] = fminf(fmaxf(__uint_as_float(w[i] & 0xffff0000u) / scale, -448.0f), 448.0f);
+        q[2 * i] = fminf(fmaxf(quot(__uint_as_float(w[i] << 16)), -448.0f), 448.0f);
+        q[2 * i + 1] = fminf(fmaxf(quot(__uint_as_float(w[i] & 0xffff0000u)), -448.0f), 448.0f);
       }
       int lo = __builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
       lo = __builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], lo, true);

@@ -168,6 +168,40 @@ def test_slab_store_two_and_three_launch_forms_agree(B, P, H, D):
     del keep3, keep2
 
 
+def test_slab_store_every_bf16_value_under_many_scales():
+    """The quantiser divides through the scale's reciprocal and one fma
+    correction; against torch's IEEE division (the reference's v / scale,
+    kv_cache.py:38-40) on the same device and against the oracle: every finite
+    bf16 value with |v| <= amax in each of 24 heads whose planted amax spans
+    1e-30 .. 1e30 (powers of two, 448, 1e-12-floor heads included)."""
+    _flush("case slab store every bf16 value")
+    B, P, H, D = 1, 512, 24, 128
+    allv = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    vals = (allv.astype(np.uint32) << 16).view(np.float32)
+    vals = vals[np.isfinite(vals)]
+    rng = np.random.default_rng(17)
+    amaxes = [1.0, 448.0, 2.0 ** -20, 2.0 ** 20, 3.0, 1e-30, 1e30, 1e-13, 5e-10, 0.1, 7.0, 1000.0]
+    amaxes += list(10.0 ** rng.uniform(-30, 30, H - len(amaxes)))
+    v = np.zeros((B, P, H, D), np.float32)
+    for h, am in enumerate(amaxes):
+        am = np.float32(torch.tensor(am).to(torch.bfloat16).float().item())
+        sel = vals[np.abs(vals) <= am]
+        head = np.resize(sel, P * D)
+        head[0] = am                                   # the amax itself
+        v[0, :, h, :] = head.reshape(P, D)
+    vb = torch.from_numpy(v).to(torch.bfloat16)
+    k = torch.zeros(B, P, H, D, dtype=torch.bfloat16)
+    cache = qik.ContiguousKVCache(1, B, P, H, D, v_fp8=True, device=DEV)
+    cache.get_layer(0).store(k.to(DEV), vb.to(DEV))
+    _, vv, sc = cache.get_layer(0).views()
+    got = vv.transpose(1, 2).contiguous().view(torch.uint8).cpu().numpy()
+    kt, vt, st = _torch_store(k.to(DEV), vb.to(DEV), True)
+    np.testing.assert_array_equal(sc.cpu().numpy(), st.cpu().numpy())
+    np.testing.assert_array_equal(got, vt.view(torch.uint8).cpu().numpy())
+    codes, scale = of.quantize_per_head(vb.float().numpy())
+    np.testing.assert_array_equal(got, codes)
+
+
 def test_slab_store_rounding_edges():
     """Quotients on e4m3fn ties and in the subnormal range, an all-zero head
     (scale 1e-12) and the extremes +-amax (codes +-448)."""
