@@ -510,7 +510,11 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, const GemmRegion&
   // the step stays one basic block.
   auto step = [&](const int kt, const int cur) __attribute__((always_inline)) {
     constexpr int NMF = C::NJ * C::MI;
-    constexpr int H = NMF / 2;  // MFMAs with reads after them
+    // reads after MFMAs [0, H), copies after MFMAs [CB, NMF); a wave with a
+    // single MFMA per step (64 x 64 tiles) issues both after it
+    constexpr int H = NMF >= 2 ? NMF / 2 : 1;
+    constexpr int CB = NMF >= 2 ? H : 0;
+    constexpr int CN = NMF - CB;
     __builtin_amdgcn_sched_barrier(0);
     wait_vmcnt<(C::NS - 3) * C::COPIES>();
     __syncthreads();
@@ -525,10 +529,10 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, const GemmRegion&
       if (idx < H) {
 #pragma unroll
         for (int r = idx * NRD / H; r < (idx + 1) * NRD / H; ++r) read_frag(kt + 1, r, fa[cur ^ 1], fw[cur ^ 1]);
-      } else {
+      }
+      if (idx >= CB) {
 #pragma unroll
-        for (int c = (idx - H) * C::COPIES / (NMF - H); c < (idx - H + 1) * C::COPIES / (NMF - H); ++c)
-          issue(sc, c);
+        for (int c = (idx - CB) * C::COPIES / CN; c < (idx - CB + 1) * C::COPIES / CN; ++c) issue(sc, c);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -664,6 +668,7 @@ int launch_quant(const qik_fp8_quant_args* a, unsigned* part, hipStream_t s) {
 typedef Cfg<256, 256, 4> Cfg256x256;
 typedef Cfg<256, 128, 4> Cfg256x128;
 typedef Cfg<128, 128, 4> Cfg128x128;
+typedef Cfg<64, 64, 4> Cfg64x64;
 
 // Time of a tile of each shape relative to a 256 x 256 tile: area / rate,
 // the rates measured on MI355X with each shape forced over whole launches
@@ -671,12 +676,17 @@ typedef Cfg<128, 128, 4> Cfg128x128;
 // 201.1 us, 4352x3072x12288 141.4 / 188.0 / 265.1 us for 256x256 / 256x128 /
 // 128x128).  A 256 x 128 tile moves 24 KiB into LDS per 512 MFMA cycles,
 // close to what the copy path sustains, so it runs at about 0.8 of the big
-// tile's rate per output, and 128 x 128 at about 0.6.
+// tile's rate per output, and 128 x 128 at about 0.6.  The 64 x 64 tile (one
+// MFMA per wave and step) is for launches with few tiles: at 256 x 3072 x
+// 12288 its 192 tiles took 45.7 us against 65.5 for 48 tiles of 128 x 128;
+// 0.3 is the rate that keeps it out of the 512- and 1024-row shapes (0.45
+// chose it there, 16-25% slower).
 struct TileShape {
   int bm, bn;
   double t;
 };
-static const TileShape kShapes[3] = {{256, 256, 1.0}, {256, 128, 0.5 / 0.8}, {128, 128, 0.25 / 0.6}};
+static const TileShape kShapes[4] = {
+    {256, 256, 1.0}, {256, 128, 0.5 / 0.8}, {128, 128, 0.25 / 0.6}, {64, 64, 0.0625 / 0.3}};
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
@@ -722,7 +732,7 @@ GemmPlan choose_plan(int64_t M, int64_t N, int cus) {
   const int64_t P = std::max(1, (cus > 0 ? cus : 256) / 8);
   GemmPlan best = {0, N};
   double best_t = 1e300;
-  for (int big = 0; big < 2; ++big) {
+  for (int big = 0; big < 3; ++big) {
     const TileShape& s1 = kShapes[big];
     const TileShape& s2 = kShapes[big + 1];
     for (int64_t k = cdiv(N, s1.bn); k >= 0; --k) {
@@ -851,7 +861,8 @@ int qik_fp8_gemm(const qik_fp8_gemm_args* a, void* stream) {
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const GemmPlan plan = choose_plan(a->M, a->N, device_cus());
   if (plan.big == 0) return launch_gemm<Cfg256x256, Cfg256x128>(p, a, plan.n1, fp16, s);
-  return launch_gemm<Cfg256x128, Cfg128x128>(p, a, plan.n1, fp16, s);
+  if (plan.big == 1) return launch_gemm<Cfg256x128, Cfg128x128>(p, a, plan.n1, fp16, s);
+  return launch_gemm<Cfg128x128, Cfg64x64>(p, a, plan.n1, fp16, s);
 }
 
 int qik_fp8_dequant(const void* w, const float* scale, void* out, int64_t n, int32_t out_dtype, void* stream) {

@@ -184,13 +184,14 @@ def _abs_sum(xq, wq, sx, sw, bias):
 @pytest.mark.parametrize("M,N,K", [
     (1536, 4096, 4096),   # 256 x 128 tiles
     (4352, 3072, 3072),   # 256 x 256 tiles
-    (300, 272, 4096),     # 128 x 128 tiles, ragged M and N
+    (300, 272, 4096),     # 64 x 64 tiles, ragged M and N
     (1, 16, 16),
     (17, 48, 80),         # K tail of 16 bytes
     (513, 1040, 1104),    # K = 17 * 64 + 16
     (256, 256, 128),
     (1543, 9232, 1104),   # 256 x 256 tiles on columns [0, 8192), 256 x 128 on the rest
     (803, 8416, 1104),    # 256 x 128 tiles on columns [0, 6400), 128 x 128 on the rest
+    (256, 1552, 3072),    # 128 x 128 or 64 x 64 tiles, ragged N
 ])
 @pytest.mark.parametrize("bias", [False, True])
 def test_gemm_vs_fp64_oracle(qik, M, N, K, bias):
@@ -295,7 +296,8 @@ def test_convert_linears_fp8_and_state_dict(qik):
 
 @pytest.mark.parametrize("M,N,K,bias", [(1536, 4096, 4096, False), (4352, 3072, 3072, True),
                                         (300, 272, 4096, True), (513, 1040, 1104, False),
-                                        (4352, 9216, 3072, True), (803, 8416, 1104, True)])
+                                        (4352, 9216, 3072, True), (803, 8416, 1104, True),
+                                        (256, 3072, 12288, True)])
 def test_gemm_matches_torch_scaled_mm(qik, M, N, K, bias):
     """torch._scaled_mm is the call the reference makes (fp8.py:87-88); on this
     device it is hipBLASLt's fp8 GEMM.  The kernel agrees with it on (almost)
