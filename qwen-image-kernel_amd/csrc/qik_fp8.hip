@@ -667,8 +667,12 @@ int launch_quant(const qik_fp8_quant_args* a, unsigned* part, hipStream_t s) {
 // GEMM tile shapes, largest first
 typedef Cfg<256, 256, 4> Cfg256x256;
 typedef Cfg<256, 128, 4> Cfg256x128;
-typedef Cfg<128, 128, 4> Cfg128x128;
-typedef Cfg<64, 64, 4> Cfg64x64;
+// The smaller tiles' k-steps are short (four and one MFMAs per wave), so they
+// keep more stages in flight to cover the copies' latency: at 256 x 3072 x
+// 12288 (64 x 64 tiles) 8 stages took 27.9 us against 45.5 with 4 (16: 28.9);
+// at 256 x 9216 x 3072 (128 x 128) 6 stages 17.0 against 18.8 with 4.
+typedef Cfg<128, 128, 6> Cfg128x128;
+typedef Cfg<64, 64, 8> Cfg64x64;
 
 // Time of a tile of each shape relative to a 256 x 256 tile: area / rate,
 // the rates measured on MI355X with each shape forced over whole launches
