@@ -23,8 +23,9 @@ batch, so it is the device time unless the host is slower) and the host time per
 (``host_us``: wall time of a loop of calls, the device running behind), priced in algorithmic HBM
 bytes against 8 TB/s, beside the same torch computation on the host CPU; and
 the W8A8 fp8 linear (FP8Linear, the DiT's projections) at the reference test's
-shape ([1536, 4096] x [4096, 4096]) and at the 1024px layer's fused QKV,
-MLP-in and MLP-out shapes (4352 tokens, H*D = 3072): GEMM device time, TFLOP/s against
+shape ([1536, 4096] x [4096, 4096]), at the 1024px layer's fused QKV,
+MLP-in and MLP-out shapes (4352 tokens, H*D = 3072) and at the text stream's
+fused QKV and MLP-out (256 tokens): GEMM device time, TFLOP/s against
 the 5.0 PF dense fp8 peak, the activation quantiser's time, the whole
 FP8Linear call through the Python API, torch._scaled_mm (hipBLASLt, the call
 the reference makes) on the same device for context, and an fp32 matmul of the
@@ -458,7 +459,9 @@ def fp8_linear_ops(qik, dev, with_cpu: bool) -> dict:
     shapes = [("fp8_linear_1536x4096x4096", 1536, 4096, 4096, "reference test shape (tests/test_fp8.py:16)"),
               ("fp8_linear_4352x9216x3072", 4352, 9216, 3072, "1024px layer, fused QKV (H*D = 3072)"),
               ("fp8_linear_4352x12288x3072", 4352, 12288, 3072, "1024px layer, MLP in (hidden 4*3072)"),
-              ("fp8_linear_4352x3072x12288", 4352, 3072, 12288, "1024px layer, MLP out (hidden 4*3072)")]
+              ("fp8_linear_4352x3072x12288", 4352, 3072, 12288, "1024px layer, MLP out (hidden 4*3072)"),
+              ("fp8_linear_256x9216x3072", 256, 9216, 3072, "text stream (256 tokens), fused QKV"),
+              ("fp8_linear_256x3072x12288", 256, 3072, 12288, "text stream (256 tokens), MLP out")]
     g = torch.Generator(device="cuda").manual_seed(78)
     for name, M, N, K, what in shapes:
         x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
