@@ -595,8 +595,12 @@ int store(const qik_slab_store_args* a, float* partial, hipStream_t s) {
   const void* fq = a->D == 128 ? (const void*)slab_quant_fp8_kernel<128> : (const void*)slab_quant_fp8_kernel<64>;
 
   if (fp8 && partial != nullptr) {
-    // K copy and the chunks' scales in one launch, then the codes
-    const int64_t ncopy = (threads + QTHREADS - 1) / QTHREADS;
+    // K copy and the chunks' scales in one launch, then the codes.  The copy
+    // blocks are rounded up to a multiple of 8 (the extra ones find no row and
+    // return), so chunk c runs on XCD c % 8 in both launches (the dispatcher
+    // deals block b to XCD b % 8): the codes launch re-reads its V rows from
+    // the L2 that the scale launch read them through.
+    const int64_t ncopy = ((threads + QTHREADS - 1) / QTHREADS + 7) / 8 * 8;
     if (ncopy + heads * chunks > (int64_t)INT_MAX) return QIK_ERR_SHAPE;
     int nc = (int)ncopy;
     void* args2[] = {&cp, &qp, &nc};
