@@ -224,6 +224,40 @@ def test_gemm_fp16_out_and_strided_rows(qik):
     _check_close(out, of.scaled_mm(xq, wq, sx, sw, bnp), _abs_sum(xq, wq, sx, sw, bnp))
 
 
+@pytest.mark.parametrize("M,N,K", [
+    (640, 512, 1024),     # 64 x 64 tiles
+    (1536, 4096, 512),    # 256 x 128 tiles
+    (4352, 3072, 256),    # 256 x 256 tiles
+    (803, 8416, 320),     # 256 x 128 then 128 x 128 columns
+    (4352, 9216, 192),    # 256 x 256 then 256 x 128 columns
+])
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16])
+def test_gemm_output_row_stride(qik, M, N, K, out_dtype):
+    """An output whose rows are ldc > N elements apart (a column slice of a
+    wider buffer) gets the same values as a contiguous one, and the columns
+    past N keep what they held: the epilogue's whole-row stores address rows
+    by ldc and stop at N."""
+    a, w, xq, wq, sx, sw = _gemm_operands(M, N, K, 300 + N)
+    sa, sb = torch.tensor([sx], device=DEV), torch.tensor([sw], device=DEV)
+    b = torch.randn(N, generator=torch.Generator().manual_seed(6)).to(out_dtype).to(DEV)
+    import ctypes
+    from qwen_image_kernel_amd import _lib
+    from qwen_image_kernel_amd import fp8 as f8
+    lib = _lib.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    want = torch.empty(M, N, dtype=out_dtype, device=DEV)
+    args = f8._gemm_args(a, w, sa, sb, b, want)
+    assert lib.qik_fp8_gemm(ctypes.byref(args), stream) == 0
+    wide = torch.full((M, N + 48), -7.0, dtype=out_dtype, device=DEV)
+    got = wide[:, :N]
+    assert got.stride(0) == N + 48
+    args = f8._gemm_args(a, w, sa, sb, b, got)
+    assert lib.qik_fp8_gemm(ctypes.byref(args), stream) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    assert (wide[:, N:] == -7.0).all()
+
+
 @pytest.mark.parametrize("M,K,N,label", [(1536, 4096, 4096, "qkv-like"), (1536, 12288, 4096, "mlp-out-like"),
                                          (4352, 3072, 3072, "H*D=3072 out"), (4352, 3072, 9216, "H*D=3072 fused qkv")])
 def test_fp8linear_matches_reference_test_bar(qik, M, K, N, label):
