@@ -177,13 +177,29 @@ __device__ __forceinline__ unsigned cvt2(float a, float b) {
   return (unsigned)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false) & 0xffffu;
 }
 
+// Weights: x / scale rounded to nearest as an IEEE division gives it, from
+// inv = RN(1/scale): q = RN(x*inv) is within an ulp of x/scale, r = x -
+// q*scale is exact (fma), and RN(q + r*inv) is the correctly rounded quotient
+// (Markstein's theorem; no overflow or underflow on the way, since |x| never
+// exceeds the amax that set the scale, so |x/scale| <= 448 (1 + 2^-22), and a
+// subnormal quotient gives a zero code either way).  The quotient takes x's
+// sign, so -0 stays -0.  A non-finite scale (an inf or NaN in the tensor) has
+// no exact remainder: the division is kept there (`exact` false).
 template <int MODE>
-__device__ __forceinline__ float quant_value(float x, float scale, float inv) {
+__device__ __forceinline__ float quant_value(float x, float scale, float inv, bool exact) {
 #pragma clang fp contract(off)
   if constexpr (MODE == QIK_FP8_ACTIVATION) {
     return x * inv;
   } else {
-    return fminf(fmaxf(x / scale, -448.0f), 448.0f);
+    float q;
+    if (exact) {
+      const float q0 = x * inv;
+      const float r = __builtin_fmaf(-q0, scale, x);
+      q = __builtin_copysignf(__builtin_fmaf(r, inv, q0), x);
+    } else {
+      q = x / scale;
+    }
+    return fminf(fmaxf(q, -448.0f), 448.0f);
   }
 }
 
@@ -212,6 +228,7 @@ __global__ void __launch_bounds__(QT) cast_kernel(const QuantParams p) {
   __syncthreads();
   const float scale = sh_scale;
   const float inv = 1.0f / scale;  // IEEE division (the reference's cast kernel: 1.0 / scale)
+  const bool ex = __builtin_isfinite(scale);
 
 #pragma unroll
   for (int u = 0; u < QU; ++u) {
@@ -221,20 +238,20 @@ __global__ void __launch_bounds__(QT) cast_kernel(const QuantParams p) {
     E::unpack(raw[u], f);
     if constexpr (PV == 8) {
       u32x2 o;
-      o.x = cvt2(quant_value<MODE>(f[0], scale, inv), quant_value<MODE>(f[1], scale, inv)) |
-            (cvt2(quant_value<MODE>(f[2], scale, inv), quant_value<MODE>(f[3], scale, inv)) << 16);
-      o.y = cvt2(quant_value<MODE>(f[4], scale, inv), quant_value<MODE>(f[5], scale, inv)) |
-            (cvt2(quant_value<MODE>(f[6], scale, inv), quant_value<MODE>(f[7], scale, inv)) << 16);
+      o.x = cvt2(quant_value<MODE>(f[0], scale, inv, ex), quant_value<MODE>(f[1], scale, inv, ex)) |
+            (cvt2(quant_value<MODE>(f[2], scale, inv, ex), quant_value<MODE>(f[3], scale, inv, ex)) << 16);
+      o.y = cvt2(quant_value<MODE>(f[4], scale, inv, ex), quant_value<MODE>(f[5], scale, inv, ex)) |
+            (cvt2(quant_value<MODE>(f[6], scale, inv, ex), quant_value<MODE>(f[7], scale, inv, ex)) << 16);
       reinterpret_cast<u32x2*>(p.out)[v] = o;
     } else {
       reinterpret_cast<unsigned*>(p.out)[v] =
-          cvt2(quant_value<MODE>(f[0], scale, inv), quant_value<MODE>(f[1], scale, inv)) |
-          (cvt2(quant_value<MODE>(f[2], scale, inv), quant_value<MODE>(f[3], scale, inv)) << 16);
+          cvt2(quant_value<MODE>(f[0], scale, inv, ex), quant_value<MODE>(f[1], scale, inv, ex)) |
+          (cvt2(quant_value<MODE>(f[2], scale, inv, ex), quant_value<MODE>(f[3], scale, inv, ex)) << 16);
     }
   }
   if (blockIdx.x == gridDim.x - 1) {
     for (int64_t i = p.nvec * PV + threadIdx.x; i < p.n; i += QT)
-      p.out[i] = (unsigned char)cvt2(quant_value<MODE>(E::get(p.x, i), scale, inv), 0.0f);
+      p.out[i] = (unsigned char)cvt2(quant_value<MODE>(E::get(p.x, i), scale, inv, ex), 0.0f);
   }
 }
 

@@ -91,6 +91,26 @@ def test_quantiser_bit_exact_vs_torch_ops(qik, shape, dtype, kind, which):
         np.testing.assert_array_equal(codes(got_q), oq)
 
 
+@pytest.mark.parametrize("amax", [1.0, 448.0, 3.0, 2.0 ** -20, 2.0 ** 20, 1e-30, 1e30, 1e-13, 5e-10, 7.0, 0.1,
+                                  1000.0])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_weight_quantiser_every_value_below_amax(qik, amax, dtype):
+    """The weight quantiser divides through the scale's reciprocal and one fma
+    correction; against torch's IEEE division (fp8.py:56-60 on the device):
+    every finite value of the dtype with |w| <= amax, amax planted."""
+    bits = torch.arange(1 << 16, dtype=torch.int32).to(torch.int16)
+    vals = bits.view(dtype).float()
+    am = torch.tensor(amax).to(dtype).float().item()
+    if not np.isfinite(am) or am == 0.0:
+        pytest.skip(f"{amax} is not a finite nonzero {dtype}")
+    sel = vals[torch.isfinite(vals) & (vals.abs() <= am)]
+    w = torch.cat([sel, torch.tensor([am])]).to(dtype).to(DEV)
+    got_q, got_s = qik.quantize_weight_tensorwise(w)
+    want_q, want_s = torch_weight_quant(w)
+    np.testing.assert_array_equal(got_s.cpu().numpy(), want_s.cpu().numpy())
+    np.testing.assert_array_equal(codes(got_q), codes(want_q))
+
+
 def test_quantiser_strided_and_misaligned_input(qik):
     base = _inputs((1537, 4096), torch.bfloat16, 5)
     x = base[1:]               # storage offset of one row: still 16-byte aligned
