@@ -690,6 +690,7 @@ typedef Cfg<256, 128, 4> Cfg256x128;
 // at 256 x 9216 x 3072 (128 x 128) 6 stages 17.0 against 18.8 with 4.
 typedef Cfg<128, 128, 6> Cfg128x128;
 typedef Cfg<64, 64, 8> Cfg64x64;
+typedef Cfg<192, 128, 4> Cfg192x128;
 
 // Time of a tile of each shape relative to a 256 x 256 tile: area / rate,
 // the rates measured on MI355X with each shape forced over whole launches
@@ -701,13 +702,17 @@ typedef Cfg<64, 64, 8> Cfg64x64;
 // MFMA per wave and step) is for launches with few tiles: at 256 x 3072 x
 // 12288 its 192 tiles took 45.7 us against 65.5 for 48 tiles of 128 x 128;
 // 0.3 is the rate that keeps it out of the 512- and 1024-row shapes (0.45
-// chose it there, 16-25% slower).
+// chose it there, 16-25% slower).  The 192 x 128 tile makes 256 tiles of
+// 1536 x 4096 (one per CU): 33.0 us against 35.6 for 192 tiles of 256 x 128,
+// a rate of about 0.65.
 struct TileShape {
   int bm, bn;
   double t;
 };
-static const TileShape kShapes[4] = {
-    {256, 256, 1.0}, {256, 128, 0.5 / 0.8}, {128, 128, 0.25 / 0.6}, {64, 64, 0.0625 / 0.3}};
+static const TileShape kShapes[5] = {
+    {256, 256, 1.0}, {256, 128, 0.5 / 0.8}, {128, 128, 0.25 / 0.6}, {64, 64, 0.0625 / 0.3}, {192, 128, 0.375 / 0.65}};
+// the (big, small) shape pairs a launch can take, as indices into kShapes
+static const int kPairs[4][2] = {{0, 1}, {1, 2}, {4, 2}, {2, 3}};
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
@@ -741,29 +746,31 @@ double xcd_makespan(int64_t t1, double d1, int64_t t2, double d2, int64_t P) {
 
 // Columns [0, n1) with tile shape `big`, [n1, N) with shape big + 1.
 struct GemmPlan {
-  int big;
+  int pair;  // index into kPairs
   int64_t n1;
 };
 
 // The split with the shortest estimated makespan on `cus` CUs.  Workgroups go
 // to the XCDs in turn, so the XCD that finishes last holds ceil(tiles / 8) of
 // each region.  The split points are whole big-tile columns; n1 = N is one
-// region of the big shape, n1 = 0 one of the next shape.
+// region of the big shape, n1 = 0 one of the small shape.  A later candidate
+// replaces an earlier one only if it is estimated 3% faster (the rates above
+// are good to a few percent); the first candidate is 256 x 256 tiles.
 GemmPlan choose_plan(int64_t M, int64_t N, int cus) {
   const int64_t P = std::max(1, (cus > 0 ? cus : 256) / 8);
   GemmPlan best = {0, N};
   double best_t = 1e300;
-  for (int big = 0; big < 3; ++big) {
-    const TileShape& s1 = kShapes[big];
-    const TileShape& s2 = kShapes[big + 1];
+  for (int pr = 0; pr < 4; ++pr) {
+    const TileShape& s1 = kShapes[kPairs[pr][0]];
+    const TileShape& s2 = kShapes[kPairs[pr][1]];
     for (int64_t k = cdiv(N, s1.bn); k >= 0; --k) {
       const int64_t n1 = std::min(k * s1.bn, N);
       const int64_t t1 = cdiv(M, s1.bm) * cdiv(n1, s1.bn);
       const int64_t t2 = cdiv(M, s2.bm) * cdiv(N - n1, s2.bn);
       const double t = xcd_makespan(cdiv(t1, 8), s1.t, cdiv(t2, 8), s2.t, P);
-      if (t < best_t * 0.999) {
+      if (t < best_t * 0.97) {
         best_t = t;
-        best = {big, n1};
+        best = {pr, n1};
       }
     }
   }
@@ -881,9 +888,12 @@ int qik_fp8_gemm(const qik_fp8_gemm_args* a, void* stream) {
   const bool fp16 = a->out_dtype == QIK_DTYPE_FP16;
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const GemmPlan plan = choose_plan(a->M, a->N, device_cus());
-  if (plan.big == 0) return launch_gemm<Cfg256x256, Cfg256x128>(p, a, plan.n1, fp16, s);
-  if (plan.big == 1) return launch_gemm<Cfg256x128, Cfg128x128>(p, a, plan.n1, fp16, s);
-  return launch_gemm<Cfg128x128, Cfg64x64>(p, a, plan.n1, fp16, s);
+  switch (plan.pair) {
+    case 0: return launch_gemm<Cfg256x256, Cfg256x128>(p, a, plan.n1, fp16, s);
+    case 1: return launch_gemm<Cfg256x128, Cfg128x128>(p, a, plan.n1, fp16, s);
+    case 2: return launch_gemm<Cfg192x128, Cfg128x128>(p, a, plan.n1, fp16, s);
+    default: return launch_gemm<Cfg128x128, Cfg64x64>(p, a, plan.n1, fp16, s);
+  }
 }
 
 int qik_fp8_dequant(const void* w, const float* scale, void* out, int64_t n, int32_t out_dtype, void* stream) {

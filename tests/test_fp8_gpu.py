@@ -250,6 +250,8 @@ def test_gemm_fp16_out_and_strided_rows(qik):
     (4352, 3072, 256),    # 256 x 256 tiles
     (803, 8416, 320),     # 256 x 128 then 128 x 128 columns
     (4352, 9216, 192),    # 256 x 256 then 256 x 128 columns
+    (1536, 4096, 256),    # 192 x 128 tiles
+    (1500, 4000, 320),    # ragged M and N
 ])
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16])
 def test_gemm_output_row_stride(qik, M, N, K, out_dtype):
