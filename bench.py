@@ -472,7 +472,10 @@ def fp8_linear_ops(qik, dev, with_cpu: bool) -> dict:
         xq, sa = f8.quantize_tensorwise(x)
         y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
         a = f8._gemm_args(xq, fq.weight, sa, fq.weight_scale, None, y)
-        us = _batch_us(lambda: lib.qik_fp8_gemm(ctypes.byref(a), stream), 30)
+        gneed = ctypes.c_int64(0)
+        _lib.check(lib.qik_fp8_gemm_workspace_size(ctypes.byref(a), ctypes.byref(gneed)), "workspace size")
+        gws = torch.empty(max(gneed.value // 4, 4), dtype=torch.float32, device=dev)
+        us = _batch_us(lambda: lib.qik_fp8_gemm_ws(ctypes.byref(a), gws.data_ptr(), gneed.value, stream), 30)
         qa = f8.quant_args(x.reshape(-1), xq, sa, _lib.FP8_ACTIVATION)
         nws = ctypes.c_int64()
         _lib.check(lib.qik_fp8_quant_workspace_size(ctypes.byref(qa), ctypes.byref(nws)), "workspace size")
@@ -480,7 +483,9 @@ def fp8_linear_ops(qik, dev, with_cpu: bool) -> dict:
         q_us = _batch_us(lambda: lib.qik_fp8_quantize(ctypes.byref(qa), qws.data_ptr(), nws.value, stream), 30)
         api_us, host_us = _batch_us(lambda: fq(x), 30), _host_us(lambda: fq(x), 100)
         flops = 2.0 * M * N * K
-        entry = {"shape_mnk": [M, N, K], "what": what, "kernel": "fp8_gemm_kernel (qik_fp8_gemm)",
+        kern = ("fp8_gemm_split_kernel + splitk_reduce_kernel (qik_fp8_gemm_ws, K split)" if gneed.value
+                else "fp8_gemm_kernel (qik_fp8_gemm_ws)")
+        entry = {"shape_mnk": [M, N, K], "what": what, "kernel": kern,
                  "us": round(us, 2), "tflops": round(flops / (us * 1e-6) / 1e12, 1),
                  "frac_fp8_peak": round(flops / (us * 1e-6) / 1e12 / PEAK_FP8_TFLOPS, 4),
                  "quantize_us": round(q_us, 2),
@@ -499,7 +504,7 @@ def fp8_linear_ops(qik, dev, with_cpu: bool) -> dict:
             entry["cpu_fp32_matmul_us"] = round(_cpu_us(lambda: xd @ wd.t(), 2), 1)
             entry["cpu_threads"] = torch.get_num_threads()
         out[name] = entry
-        del x, lin, fq, xq, y
+        del x, lin, fq, xq, y, gws
     return out
 
 

@@ -44,7 +44,8 @@ enum qik_fp8_mode {
  * Python scalar is multiplied by the scalar's fp32 reciprocal there.  The
  * activation form takes the reciprocal of the scale once (IEEE fp32 division)
  * and multiplies, as the reference's cast kernel does; the weight form divides
- * every element (IEEE) and clamps, as the reference's weight quantiser does.
+ * every element (the correctly rounded quotient of an IEEE division) and
+ * clamps, as the reference's weight quantiser does.
  * Both round to nearest even.  Finite inputs give codes bit-identical to those
  * torch ops on the device; a non-finite input makes the scale non-finite and
  * the codes NaN or zero, as in the reference ("non-finite inputs poison the
@@ -95,6 +96,20 @@ typedef struct qik_fp8_gemm_args {
 
 int qik_fp8_gemm_validate(const qik_fp8_gemm_args* args);
 int qik_fp8_gemm(const qik_fp8_gemm_args* args, void* stream);
+
+/* The same product with a workspace (no counterpart in the reference, whose
+ * torch._scaled_mm call, fp8.py:87-88, gets its scratch from hipBLASLt): a
+ * launch with few output tiles and a long K (the text stream's 256-token MLP
+ * out, 256 x 3072 x 12288) splits K into up to 8 slices whose fp32 sums go
+ * into the workspace and are added in slice order by a second launch.  The
+ * sums then round differently from the one-pass product (within an fp32
+ * accumulation bound; the output differs in the last bit on a small share of
+ * elements).  qik_fp8_gemm_workspace_size gives the bytes the call needs: 0
+ * when it does not split, and then qik_fp8_gemm_ws is qik_fp8_gemm (the
+ * workspace may be NULL).  Otherwise the workspace must be 16-byte aligned and
+ * at least that size (QIK_ERR_WORKSPACE); its contents are irrelevant. */
+int qik_fp8_gemm_workspace_size(const qik_fp8_gemm_args* args, int64_t* bytes);
+int qik_fp8_gemm_ws(const qik_fp8_gemm_args* args, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* out[i] = round(fp32(code[i]) * scale[0]) into out_dtype (bf16 or fp16), for
  * i < n: the dequantised weight of the bf16 path (fp8.py:81: fp8 -> bf16 ->

@@ -231,6 +231,10 @@ EXPORTS = (
      (ctypes.POINTER(QikFp8QuantArgs), ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p)),
     ("qik_fp8_gemm_validate", ctypes.c_int, (ctypes.POINTER(QikFp8GemmArgs),)),
     ("qik_fp8_gemm", ctypes.c_int, (ctypes.POINTER(QikFp8GemmArgs), ctypes.c_void_p)),
+    ("qik_fp8_gemm_workspace_size", ctypes.c_int,
+     (ctypes.POINTER(QikFp8GemmArgs), ctypes.POINTER(ctypes.c_int64))),
+    ("qik_fp8_gemm_ws", ctypes.c_int,
+     (ctypes.POINTER(QikFp8GemmArgs), ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p)),
     ("qik_fp8_dequant", ctypes.c_int,
      (ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p)),
 )

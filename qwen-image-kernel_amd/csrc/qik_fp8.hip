@@ -37,6 +37,7 @@ typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((__vector_size__(2 * sizeof(__bf16))));
 typedef _Float16 f16x2 __attribute__((__vector_size__(2 * sizeof(_Float16))));
 
@@ -343,6 +344,8 @@ struct GemmParams {
   int lda, ldw;   // bytes
   int64_t ldc;    // elements
   GemmRegion r[2];  // columns [0, n1) with the larger tile, then [n1, N)
+  int ksplit;       // split launches: k-slices per tile (region 0 only)
+  float* partial;   // split launches: [ksplit][M][N] fp32 sums of each slice
 };
 
 template <int BM_, int BN_, int NS_, int WGM_ = 2, int WGN_ = 2>
@@ -400,9 +403,11 @@ __device__ __forceinline__ int swz(int r) { return (r >> 2) & 3; }
 
 // One BM x BN output tile of region g; bx counts the region's workgroups
 // (bx % 8 is the XCD: every region starts at a multiple of 8).
-template <class C, bool FP16>
+// SPLIT: the workgroup sums k-steps [kb, ke) of slice `slice` and writes the
+// fp32 sums to p.partial instead of the outputs.
+template <class C, bool FP16, bool SPLIT = false>
 __device__ __forceinline__ void gemm_tile(const GemmParams& p, const GemmRegion& rg, const int bx,
-                                          unsigned char* lds) {
+                                          unsigned char* lds, const int slice = 0) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: copy targets go to SGPRs
@@ -439,7 +444,9 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, const GemmRegion&
   const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_ptr_t)lds;
   const unsigned char* abase = p.a + (int64_t)m0 * p.lda;
   const unsigned char* wbase = rg.w + (int64_t)n0 * p.ldw;
-  const int nk = (p.K + KB - 1) / KB;
+  const int nkall = (p.K + KB - 1) / KB;
+  const int kb = SPLIT ? (int)((int64_t)nkall * slice / p.ksplit) : 0;
+  const int nk = SPLIT ? (int)((int64_t)nkall * (slice + 1) / p.ksplit) : nkall;  // end of the k-steps
 
   // copy state of one k-step: the stage's LDS address and the two buffer
   // resources; past the end of K a lane's chunk would read the next row, so
@@ -509,11 +516,11 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, const GemmRegion&
 
   // prologue: stages 0 .. NS-2 in flight, stage 0 published, its fragments read
 #pragma unroll
-  for (int s0 = 0; s0 < C::NS - 1; ++s0) copy_stage(s0);
+  for (int s0 = 0; s0 < C::NS - 1; ++s0) copy_stage(kb + s0);
   wait_vmcnt<(C::NS - 2) * C::COPIES>();
   __syncthreads();
   i32x8 fa[2][C::MI], fw[2][C::NJ];
-  read_frags(0, fa[0], fw[0]);
+  read_frags(kb, fa[0], fw[0]);
 
   // k-step kt: publish stage kt+1 (its copies done, and every wave past its
   // MFMAs of kt-1, so stage kt-1 = kt+NS-1 is free), then run the MFMAs of kt
@@ -554,7 +561,7 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, const GemmRegion&
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-  int kt = 0;
+  int kt = kb;
   for (; kt + 1 < nk; kt += 2) {
     step(kt, 0);
     step(kt + 1, 1);
@@ -572,6 +579,26 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, const GemmRegion&
   constexpr int RPI = 64 / CPR;   // rows per store instruction
   static_assert(C::BM * RB <= C::NS * C::STAGE, "the output tile fits the stages");
   wait_vmcnt<0>();  // the copies of the steps past the end still land in their stages
+  if constexpr (SPLIT) {
+    // the slice's fp32 sums, 4 columns of one row per lane and register quad
+    float* dst = p.partial + (int64_t)slice * p.M * rg.N;
+#pragma unroll
+    for (int j = 0; j < C::NJ; ++j) {
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd) {
+        const int n = n0 + wn * C::WN + j * 32 + qd * 8 + (lane >> 5) * 4;
+#pragma unroll
+        for (int i = 0; i < C::MI; ++i) {
+          const int m = m0 + wm * C::WM + i * 32 + (lane & 31);
+          if (m < p.M && n < rg.N) {
+            const f32x4 v = {acc[j][i][qd * 4], acc[j][i][qd * 4 + 1], acc[j][i][qd * 4 + 2], acc[j][i][qd * 4 + 3]};
+            *reinterpret_cast<f32x4*>(dst + (int64_t)m * rg.N + n) = v;
+          }
+        }
+      }
+    }
+    return;
+  }
   __syncthreads();  // and every wave is done with the last stage's fragments
   {
 #pragma clang fp contract(off)
@@ -629,6 +656,63 @@ fp8_gemm_kernel(const GemmParams p) {
   const int bx = blockIdx.x;
   if (bx < p.r[0].wgs) gemm_tile<C1, FP16>(p, p.r[0], bx, lds);
   else gemm_tile<C2, FP16>(p, p.r[1], bx - p.r[0].wgs, lds);
+}
+
+// Split launch: workgroup b sums k-slice b / wgs of tile b % wgs of region 0
+// (wgs a multiple of 8, so a tile's slices all run on one XCD).
+template <class C, bool FP16>
+__global__ void __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::NW / 4, C::NW / 4)))
+fp8_gemm_split_kernel(const GemmParams p) {
+  __shared__ __attribute__((aligned(1024))) unsigned char lds[C::NS * C::STAGE];
+  const int wgs = p.r[0].wgs;
+  const int bx = blockIdx.x;
+  gemm_tile<C, FP16, true>(p, p.r[0], bx % wgs, lds, bx / wgs);
+}
+
+// out[m][n..n+7] = round((sum over the slices, in slice order) * (sa * sw)
+// + bias[n..n+7]), 8 outputs per thread.
+template <bool FP16>
+__global__ void __launch_bounds__(256) splitk_reduce_kernel(const GemmParams p) {
+#pragma clang fp contract(off)
+  const GemmRegion& rg = p.r[0];
+  const int per_row = rg.N / 8;
+  const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (g >= (int64_t)p.M * per_row) return;
+  const int m = (int)(g / per_row);
+  const int n = (int)(g - (int64_t)m * per_row) * 8;
+  const int64_t slice_elems = (int64_t)p.M * rg.N;
+  const float* src = p.partial + (int64_t)m * rg.N + n;
+  f32x4 lo = *reinterpret_cast<const f32x4*>(src);
+  f32x4 hi = *reinterpret_cast<const f32x4*>(src + 4);
+  for (int sl = 1; sl < p.ksplit; ++sl) {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(src + sl * slice_elems);
+    const f32x4 b = *reinterpret_cast<const f32x4*>(src + sl * slice_elems + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      lo[e] = lo[e] + a[e];
+      hi[e] = hi[e] + b[e];
+    }
+  }
+  const float ab = p.sa[0] * p.sw[0];
+  float bv[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+  if (rg.bias != nullptr) {  // the bias is 8-byte aligned
+    const u32x2 b0 = *reinterpret_cast<const u32x2*>(rg.bias + (int64_t)n * 2);
+    const u32x2 b1 = *reinterpret_cast<const u32x2*>(rg.bias + (int64_t)n * 2 + 8);
+    unpack2<FP16>(b0.x, bv[0], bv[1]);
+    unpack2<FP16>(b0.y, bv[2], bv[3]);
+    unpack2<FP16>(b1.x, bv[4], bv[5]);
+    unpack2<FP16>(b1.y, bv[6], bv[7]);
+  }
+  float y[8];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    y[e] = lo[e] * ab;
+    y[e] = y[e] + bv[e];
+    y[e + 4] = hi[e] * ab;
+    y[e + 4] = y[e + 4] + bv[e + 4];
+  }
+  const u32x4 o = {pack2<FP16>(y[0], y[1]), pack2<FP16>(y[2], y[3]), pack2<FP16>(y[4], y[5]), pack2<FP16>(y[6], y[7])};
+  *reinterpret_cast<u32x4*>(rg.out + ((int64_t)m * p.ldc + n) * 2) = o;
 }
 
 }  // namespace qik_fp8
@@ -748,6 +832,7 @@ double xcd_makespan(int64_t t1, double d1, int64_t t2, double d2, int64_t P) {
 struct GemmPlan {
   int pair;  // index into kPairs
   int64_t n1;
+  double t;  // estimated makespan, in 256 x 256 tile times
 };
 
 // The split with the shortest estimated makespan on `cus` CUs.  Workgroups go
@@ -758,7 +843,7 @@ struct GemmPlan {
 // are good to a few percent); the first candidate is 256 x 256 tiles.
 GemmPlan choose_plan(int64_t M, int64_t N, int cus) {
   const int64_t P = std::max(1, (cus > 0 ? cus : 256) / 8);
-  GemmPlan best = {0, N};
+  GemmPlan best = {0, N, 0.0};
   double best_t = 1e300;
   for (int pr = 0; pr < 4; ++pr) {
     const TileShape& s1 = kShapes[kPairs[pr][0]];
@@ -770,11 +855,31 @@ GemmPlan choose_plan(int64_t M, int64_t N, int cus) {
       const double t = xcd_makespan(cdiv(t1, 8), s1.t, cdiv(t2, 8), s2.t, P);
       if (t < best_t * 0.97) {
         best_t = t;
-        best = {pr, n1};
+        best = {pr, n1, t};
       }
     }
   }
+  best.t = best_t;
   return best;
+}
+
+// K-split of a launch with few tiles and many k-steps: S slices of 128 x 128
+// tiles, each summing nk / S k-steps into fp32 partials that a second launch
+// adds in slice order.  Only when it is estimated well ahead of the unsplit
+// plan (the partials, the second launch and the shorter pipelines cost
+// something): at least 96 k-steps, at most half the CUs' worth of tiles.
+// 1 means no split.
+int choose_ksplit(int64_t M, int64_t N, int64_t K, int cus) {
+  if (cus <= 0) cus = 256;
+  const int64_t nk = cdiv(K, KB);
+  if (nk < 96) return 1;
+  const int64_t t128 = cdiv(M, 128) * cdiv(N, 128);
+  if (t128 * 2 > cus) return 1;
+  const int S = (int)std::min<int64_t>({cus / t128, 8, nk / 16});
+  if (S < 2) return 1;
+  const int64_t P = std::max(1, cus / 8);
+  const double t_split = xcd_makespan(cdiv(t128 * S, 8), kShapes[2].t / S, 0, 0.0, P);
+  return t_split < 0.6 * choose_plan(M, N, cus).t ? S : 1;
 }
 
 // tile rows per group of the tile order: the group size that minimises the
@@ -894,6 +999,52 @@ int qik_fp8_gemm(const qik_fp8_gemm_args* a, void* stream) {
     case 2: return launch_gemm<Cfg192x128, Cfg128x128>(p, a, plan.n1, fp16, s);
     default: return launch_gemm<Cfg128x128, Cfg64x64>(p, a, plan.n1, fp16, s);
   }
+}
+
+int qik_fp8_gemm_workspace_size(const qik_fp8_gemm_args* a, int64_t* bytes) {
+  using namespace qik_fp8;
+  if (bytes == nullptr) return QIK_ERR_NULL_ARG;
+  *bytes = 0;
+  const int st = qik_fp8_gemm_validate(a);
+  if (st != QIK_OK) return st;
+  const int S = choose_ksplit(a->M, a->N, a->K, device_cus());
+  if (S > 1) *bytes = (int64_t)S * a->M * a->N * (int64_t)sizeof(float);
+  return QIK_OK;
+}
+
+int qik_fp8_gemm_ws(const qik_fp8_gemm_args* a, void* workspace, int64_t workspace_bytes, void* stream) {
+  using namespace qik_fp8;
+  const int st = qik_fp8_gemm_validate(a);
+  if (st != QIK_OK) return st;
+  const int S = choose_ksplit(a->M, a->N, a->K, device_cus());
+  if (S <= 1) return qik_fp8_gemm(a, stream);
+  const int64_t need = (int64_t)S * a->M * a->N * (int64_t)sizeof(float);
+  if (workspace == nullptr || workspace_bytes < need || !aligned_to(workspace, 16)) return QIK_ERR_WORKSPACE;
+  GemmParams p;
+  memset(&p, 0, sizeof(p));
+  p.a = static_cast<const unsigned char*>(a->a);
+  p.sa = a->scale_a;
+  p.sw = a->scale_w;
+  p.M = (int)a->M;
+  p.K = (int)a->K;
+  p.lda = (int)a->lda;
+  p.ldw = (int)a->ldw;
+  p.ldc = a->ldc;
+  p.ksplit = S;
+  p.partial = static_cast<float*>(workspace);
+  if (set_region<Cfg128x128>(p.r[0], a, 0, a->N) != QIK_OK) return QIK_ERR_SHAPE;
+  const int64_t grid = (int64_t)p.r[0].wgs * S;
+  const int64_t rgrid = (a->M * (a->N / 8) + 255) / 256;
+  if (grid > (int64_t)INT_MAX || rgrid > (int64_t)INT_MAX) return QIK_ERR_SHAPE;
+  const bool fp16 = a->out_dtype == QIK_DTYPE_FP16;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  void* args[] = {&p};
+  const void* fk = fp16 ? (const void*)fp8_gemm_split_kernel<Cfg128x128, true>
+                        : (const void*)fp8_gemm_split_kernel<Cfg128x128, false>;
+  if (hipLaunchKernel(fk, dim3((unsigned)grid), dim3(Cfg128x128::NT), args, 0, s) != hipSuccess)
+    return QIK_ERR_LAUNCH;
+  const void* fr = fp16 ? (const void*)splitk_reduce_kernel<true> : (const void*)splitk_reduce_kernel<false>;
+  return hipLaunchKernel(fr, dim3((unsigned)rgrid), dim3(256), args, 0, s) == hipSuccess ? QIK_OK : QIK_ERR_LAUNCH;
 }
 
 int qik_fp8_dequant(const void* w, const float* scale, void* out, int64_t n, int32_t out_dtype, void* stream) {

@@ -52,6 +52,7 @@ _OUT_DTYPES = {torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_FP16}
 # partial-maximum workspace of the quantiser, one per (device, stream); the
 # kernels write every word they read, so it is never cleared
 _QUANT_WS: dict = {}
+_GEMM_WS: dict = {}   # (device index, stream) -> fp32 workspace of the K-split GEMMs
 
 
 def _stream(dev: torch.device) -> int:
@@ -66,6 +67,21 @@ def _quant_workspace(dev: torch.device, stream: int, nbytes: int) -> torch.Tenso
             _QUANT_WS.clear()
         ws = _QUANT_WS[key] = torch.empty(max(nbytes // 4, 1024), dtype=torch.int32, device=dev)
     return ws
+
+
+def _gemm_workspace(dev: torch.device, stream: int, nbytes: int) -> int:
+    """Address of a workspace of at least nbytes for qik_fp8_gemm_ws on this
+    stream (0 when the call needs none).  One per (device, stream), grown as
+    needed: calls on one stream run in order, so they can share it."""
+    if nbytes <= 0:
+        return 0
+    key = (dev.index, stream)
+    ws = _GEMM_WS.get(key)
+    if ws is None or ws.numel() * 4 < nbytes:
+        if len(_GEMM_WS) >= 64:
+            _GEMM_WS.clear()
+        ws = _GEMM_WS[key] = torch.empty((nbytes + 3) // 4, dtype=torch.float32, device=dev)
+    return ws.data_ptr()
 
 
 def quant_args(flat: torch.Tensor, out: torch.Tensor, scale: torch.Tensor, mode: int) -> _lib.QikFp8QuantArgs:
@@ -202,7 +218,11 @@ def fp8_linear(
     a = _gemm_args(xq, w, sa, sw, b, out)
     lib = _lib.load()
     with torch.cuda.device(dev):
-        _lib.check(lib.qik_fp8_gemm(ctypes.byref(a), _stream(dev)), "qik_fp8_gemm")
+        need = ctypes.c_int64(0)
+        _lib.check(lib.qik_fp8_gemm_workspace_size(ctypes.byref(a), ctypes.byref(need)), "qik_fp8_gemm")
+        stream = _stream(dev)
+        ws = _gemm_workspace(dev, stream, need.value)
+        _lib.check(lib.qik_fp8_gemm_ws(ctypes.byref(a), ws or None, need.value, stream), "qik_fp8_gemm")
     return out
 
 
@@ -210,8 +230,8 @@ class _LinearCall:
     """What one FP8Linear.forward key (input geometry, weight, scale and bias
     tensors and their versions) needs at call time."""
 
-    __slots__ = ("fast", "index", "xq_shape", "out_shape", "result_shape", "ws_bytes", "qargs", "gargs", "quantize",
-                 "gemm", "keep")
+    __slots__ = ("fast", "index", "xq_shape", "out_shape", "result_shape", "ws_bytes", "gws_bytes", "qargs", "gargs",
+                 "quantize", "gemm", "keep")
 
 
 def _prepare_linear(x, weight, wscale, bias, out_features) -> _LinearCall:
@@ -246,9 +266,11 @@ def _prepare_linear(x, weight, wscale, bias, out_features) -> _LinearCall:
                "qik_fp8_quant_workspace_size")
     c.ws_bytes = need.value
     c.gargs = _gemm_args(xq, weight, s_a, wscale, bias, out)
-    _lib.check(lib.qik_fp8_gemm_validate(ctypes.byref(c.gargs)), "qik_fp8_gemm")
+    need = ctypes.c_int64(0)
+    _lib.check(lib.qik_fp8_gemm_workspace_size(ctypes.byref(c.gargs), ctypes.byref(need)), "qik_fp8_gemm")
+    c.gws_bytes = need.value
     c.quantize = lib.qik_fp8_quantize
-    c.gemm = lib.qik_fp8_gemm
+    c.gemm = lib.qik_fp8_gemm_ws
     return c
 
 
@@ -306,7 +328,8 @@ class FP8Linear(nn.Module):
             ga.a = xq.data_ptr()
             ga.scale_a = s_a.data_ptr()
             ga.out = out.data_ptr()
-            _lib.check(ent.gemm(ctypes.byref(ga), stream), "qik_fp8_gemm")
+            gws = _gemm_workspace(x.device, stream, ent.gws_bytes)
+            _lib.check(ent.gemm(ctypes.byref(ga), gws or None, ent.gws_bytes, stream), "qik_fp8_gemm")
         else:
             x2 = x.reshape(-1, x.shape[-1])
             xq, s_a = quantize_tensorwise(x2)

@@ -357,6 +357,30 @@ def test_fp8_gemm_validate(kw, code):
     assert _lib.load().qik_fp8_gemm_validate(ctypes.byref(_gemm_args(**kw))) == code
 
 
+def test_fp8_gemm_workspace_size_and_checks():
+    """The workspace variant splits K only for few tiles and a long K: the
+    reference test's shape needs none; the text stream's MLP out (256 tokens,
+    K = 12288) takes 5 slices of 48 tiles of 128 x 128 (on 256 CUs, the count
+    the host assumes when it cannot ask a device) in fp32."""
+    lib = _lib.load()
+    n = ctypes.c_int64(-1)
+    assert lib.qik_fp8_gemm_workspace_size(ctypes.byref(_gemm_args()), ctypes.byref(n)) == 0
+    assert n.value == 0
+    skinny = dict(M=256, N=3072, K=12288, lda=12288, ldw=12288, ldc=3072)
+    assert lib.qik_fp8_gemm_workspace_size(ctypes.byref(_gemm_args(**skinny)), ctypes.byref(n)) == 0
+    assert n.value == 5 * 256 * 3072 * 4
+    assert lib.qik_fp8_gemm_workspace_size(ctypes.byref(_gemm_args(M=0)), ctypes.byref(n)) == -5
+    assert lib.qik_fp8_gemm_workspace_size(ctypes.byref(_gemm_args()), None) == -1
+    buf = (ctypes.c_uint8 * 64)()
+    base = (ctypes.addressof(buf) + 15) // 16 * 16
+    WS = -12
+    a = _gemm_args(**skinny)
+    assert lib.qik_fp8_gemm_ws(ctypes.byref(a), None, n.value, None) == WS
+    assert lib.qik_fp8_gemm_ws(ctypes.byref(a), base, 32, None) == WS
+    assert lib.qik_fp8_gemm_ws(ctypes.byref(a), base + 8, n.value, None) == WS
+    assert lib.qik_fp8_gemm_ws(ctypes.byref(_gemm_args(M=0)), base, n.value, None) == -5
+
+
 def _quant_args(**kw):
     a = _lib.QikFp8QuantArgs()
     a.abi_version = _lib.ABI_VERSION

@@ -202,13 +202,15 @@ def _abs_sum(xq, wq, sx, sw, bias):
 
 
 @pytest.mark.parametrize("M,N,K", [
-    (1536, 4096, 4096),   # 256 x 128 tiles
+    (1536, 4096, 4096),   # 192 x 128 tiles
     (4352, 3072, 3072),   # 256 x 256 tiles
     (300, 272, 4096),     # 64 x 64 tiles, ragged M and N
     (1, 16, 16),
     (17, 48, 80),         # K tail of 16 bytes
     (513, 1040, 1104),    # K = 17 * 64 + 16
     (256, 256, 128),
+    (256, 3072, 12288),   # K split in 5 (through the workspace variant)
+    (100, 1040, 8192),    # K split in 8, ragged M and N
     (1543, 9232, 1104),   # 256 x 256 tiles on columns [0, 8192), 256 x 128 on the rest
     (803, 8416, 1104),    # 256 x 128 tiles on columns [0, 6400), 128 x 128 on the rest
     (256, 1552, 3072),    # 128 x 128 or 64 x 64 tiles, ragged N
@@ -252,6 +254,8 @@ def test_gemm_fp16_out_and_strided_rows(qik):
     (4352, 9216, 192),    # 256 x 256 then 256 x 128 columns
     (1536, 4096, 256),    # 192 x 128 tiles
     (1500, 4000, 320),    # ragged M and N
+    (256, 3072, 12288),   # K split in 5 (workspace variant)
+    (100, 1040, 8192),    # K split in 8, ragged M and N
 ])
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16])
 def test_gemm_output_row_stride(qik, M, N, K, out_dtype):
@@ -269,12 +273,15 @@ def test_gemm_output_row_stride(qik, M, N, K, out_dtype):
     stream = torch.cuda.current_stream().cuda_stream
     want = torch.empty(M, N, dtype=out_dtype, device=DEV)
     args = f8._gemm_args(a, w, sa, sb, b, want)
-    assert lib.qik_fp8_gemm(ctypes.byref(args), stream) == 0
+    need = ctypes.c_int64(0)
+    assert lib.qik_fp8_gemm_workspace_size(ctypes.byref(args), ctypes.byref(need)) == 0
+    ws = torch.full((max(need.value // 4, 4),), float("nan"), dtype=torch.float32, device=DEV)  # garbage
+    assert lib.qik_fp8_gemm_ws(ctypes.byref(args), ws.data_ptr(), need.value, stream) == 0
     wide = torch.full((M, N + 48), -7.0, dtype=out_dtype, device=DEV)
     got = wide[:, :N]
     assert got.stride(0) == N + 48
     args = f8._gemm_args(a, w, sa, sb, b, got)
-    assert lib.qik_fp8_gemm(ctypes.byref(args), stream) == 0
+    assert lib.qik_fp8_gemm_ws(ctypes.byref(args), ws.data_ptr(), need.value, stream) == 0
     torch.cuda.synchronize()
     assert torch.equal(got.view(torch.int16), want.view(torch.int16))
     assert (wide[:, N:] == -7.0).all()
