@@ -52,8 +52,8 @@ int qik_rms_rope(const qik_rms_rope_args* args, void* stream);
 /* One layer's prefix K/V into the slab (layout [B, H, P_max, D] per layer):
  *   k_dst[b, h, p, :] = k[b, p, h, :]
  *   bf16/fp16 V:  v_dst[b, h, p, :] = v[b, p, h, :]
- *   fp8 V (v_fp8 != 0, bf16 only), per (b, h) over all p < P and d:
- *     amax  = max |v|                     (fp32)
+ *   fp8 V (v_fp8 != 0; v bf16 or fp16), per (b, h) over all p < P and d:
+ *     amax  = max |fp32(v)|
  *     scale = max(amax * fp32(1/448), fp32(1e-12))
  *     v_dst = e4m3fn_rne(clamp(v / scale, -448, 448))   (IEEE fp32 division)
  *     v_scale[b*H + h] = scale

@@ -265,7 +265,7 @@ __global__ void __launch_bounds__(NTHREADS) slab_copy_kernel(const CopyParams p)
 //     scale into the workspace, then slab_quant_fp8_kernel takes the largest of
 //     its head's and writes the codes and the scale (two launches).
 struct QuantParams {
-  const char* v;     // bf16 [B, P, H, D]
+  const char* v;     // bf16 or fp16 [B, P, H, D]
   char* dst;         // fp8 slab V of the layer
   float* scale;      // [B*H]
   float* partial;    // workspace launches: [B*H*chunks] scales of each chunk's rows (else NULL)
@@ -278,8 +278,8 @@ constexpr int QTHREADS = 512;
 constexpr int MAX_SCALE_CHUNKS = 64;   // scale chunks per head at most: the workspace holds this many per head
 
 // max(amax * fp32(1/448), 1e-12) of the rows of chunk bx = bh * chunks + c,
-// valid in thread 0 (a block of QTHREADS threads)
-template <int D>
+// valid in thread 0 (a block of QTHREADS threads); FP16: the rows are fp16, else bf16
+template <int D, bool FP16>
 __device__ __forceinline__ float chunk_scale(const QuantParams& p, const int bx) {
   constexpr int TPR = D / 8;             // threads per row
   constexpr int RPS = QTHREADS / TPR;    // rows per step
@@ -301,8 +301,10 @@ __device__ __forceinline__ float chunk_scale(const QuantParams& p, const int bx)
     const unsigned w[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      amax = fmaxf(amax, fabsf(__uint_as_float(w[i] << 16)));
-      amax = fmaxf(amax, fabsf(__uint_as_float(w[i] & 0xffff0000u)));
+      float lo, hi;
+      unpack2<FP16>(w[i], lo, hi);
+      amax = fmaxf(amax, fabsf(lo));
+      amax = fmaxf(amax, fabsf(hi));
     }
   };
   // U rows per batch, all loads issued before the first is used; rows past
@@ -332,9 +334,9 @@ __device__ __forceinline__ float chunk_scale(const QuantParams& p, const int bx)
   return sc;
 }
 
-template <int D>
+template <int D, bool FP16>
 __global__ void __launch_bounds__(QTHREADS) slab_scale_fp8_kernel(const QuantParams p) {
-  const float sc = chunk_scale<D>(p, blockIdx.x);
+  const float sc = chunk_scale<D, FP16>(p, blockIdx.x);
   // non-negative fp32 values order like their bit patterns
   if (threadIdx.x == 0) atomicMax(reinterpret_cast<unsigned*>(p.scale) + blockIdx.x / p.chunks, __float_as_uint(sc));
 }
@@ -342,7 +344,7 @@ __global__ void __launch_bounds__(QTHREADS) slab_scale_fp8_kernel(const QuantPar
 // Workspace form, first launch: blocks [0, ncopy) copy K (QTHREADS 16-byte
 // chunks each), the others write their chunk's scale into p.partial.  Every
 // partial is written, so the workspace needs no clearing.
-template <int D>
+template <int D, bool FP16>
 __global__ void __launch_bounds__(QTHREADS) slab_copy_scale_kernel(const CopyParams cp, const QuantParams p,
                                                                    const int ncopy) {
   if ((int)blockIdx.x < ncopy) {
@@ -352,11 +354,11 @@ __global__ void __launch_bounds__(QTHREADS) slab_copy_scale_kernel(const CopyPar
     return;
   }
   const int bx = (int)blockIdx.x - ncopy;
-  const float sc = chunk_scale<D>(p, bx);
+  const float sc = chunk_scale<D, FP16>(p, bx);
   if (threadIdx.x == 0) p.partial[bx] = sc;
 }
 
-template <int D>
+template <int D, bool FP16>
 __global__ void __launch_bounds__(QTHREADS) slab_quant_fp8_kernel(const QuantParams p) {
 #pragma clang fp contract(off)
   constexpr int TPR = D / 8;             // threads per row
@@ -423,8 +425,10 @@ __global__ void __launch_bounds__(QTHREADS) slab_quant_fp8_kernel(const QuantPar
       float q[8];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        q[2 * i] = fminf(fmaxf(quot(__uint_as_float(w[i] << 16)), -448.0f), 448.0f);
-        q[2 * i + 1] = fminf(fmaxf(quot(__uint_as_float(w[i] & 0xffff0000u)), -448.0f), 448.0f);
+        float lo, hi;
+        unpack2<FP16>(w[i], lo, hi);
+        q[2 * i] = fminf(fmaxf(quot(lo), -448.0f), 448.0f);
+        q[2 * i + 1] = fminf(fmaxf(quot(hi), -448.0f), 448.0f);
       }
       int lo = __builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
       lo = __builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], lo, true);
@@ -524,7 +528,6 @@ int validate_store(const qik_slab_store_args* a, int64_t* rows) {
   if (a->abi_version != QIK_ABI_VERSION || a->reserved0 != 0) return QIK_ERR_ABI_VERSION;
   if (a->dtype != QIK_DTYPE_BF16 && a->dtype != QIK_DTYPE_FP16) return QIK_ERR_DTYPE;
   const bool fp8 = a->v_fp8 != 0;
-  if (fp8 && a->dtype != QIK_DTYPE_BF16) return QIK_ERR_FP8_SCALE;
   if (fp8 != (a->v_scale != nullptr)) return QIK_ERR_FP8_SCALE;
   if (a->D != 64 && a->D != 128) return QIK_ERR_HEAD_DIM;
   if (!sizes_ok(a->B, a->P, a->H, a->D)) return QIK_ERR_SHAPE;
@@ -592,7 +595,14 @@ int store(const qik_slab_store_args* a, float* partial, hipStream_t s) {
   chunks = std::max<int64_t>(1, std::min<int64_t>({chunks, (int64_t)MAX_SCALE_CHUNKS, a->P / 32}));
   qp.chunks = (int)chunks;
   void* qargs[] = {&qp};
-  const void* fq = a->D == 128 ? (const void*)slab_quant_fp8_kernel<128> : (const void*)slab_quant_fp8_kernel<64>;
+  // the fp8 kernels per head size and source type (bf16 or fp16 V)
+  const bool f16 = a->dtype == QIK_DTYPE_FP16;
+  const int kix = (a->D == 128 ? 0 : 2) + (f16 ? 1 : 0);
+  const void* const quant_fns[4] = {(const void*)slab_quant_fp8_kernel<128, false>,
+                                    (const void*)slab_quant_fp8_kernel<128, true>,
+                                    (const void*)slab_quant_fp8_kernel<64, false>,
+                                    (const void*)slab_quant_fp8_kernel<64, true>};
+  const void* fq = quant_fns[kix];
 
   if (fp8 && partial != nullptr) {
     // K copy and the chunks' scales in one launch, then the codes.  The copy
@@ -604,7 +614,11 @@ int store(const qik_slab_store_args* a, float* partial, hipStream_t s) {
     if (ncopy + heads * chunks > (int64_t)INT_MAX) return QIK_ERR_SHAPE;
     int nc = (int)ncopy;
     void* args2[] = {&cp, &qp, &nc};
-    const void* fc = a->D == 128 ? (const void*)slab_copy_scale_kernel<128> : (const void*)slab_copy_scale_kernel<64>;
+    const void* const copy_scale_fns[4] = {(const void*)slab_copy_scale_kernel<128, false>,
+                                           (const void*)slab_copy_scale_kernel<128, true>,
+                                           (const void*)slab_copy_scale_kernel<64, false>,
+                                           (const void*)slab_copy_scale_kernel<64, true>};
+    const void* fc = copy_scale_fns[kix];
     if (hipLaunchKernel(fc, dim3((unsigned)(ncopy + heads * chunks)), dim3(QTHREADS), args2, 0, s) != hipSuccess)
       return QIK_ERR_LAUNCH;
     return hipLaunchKernel(fq, dim3((unsigned)(heads * chunks)), dim3(QTHREADS), qargs, 0, s) == hipSuccess
@@ -616,7 +630,11 @@ int store(const qik_slab_store_args* a, float* partial, hipStream_t s) {
                                  dim3(NTHREADS), cargs, 0, s);
   if (e != hipSuccess) return QIK_ERR_LAUNCH;
   if (!fp8) return QIK_OK;
-  const void* fs = a->D == 128 ? (const void*)slab_scale_fp8_kernel<128> : (const void*)slab_scale_fp8_kernel<64>;
+  const void* const scale_fns[4] = {(const void*)slab_scale_fp8_kernel<128, false>,
+                                    (const void*)slab_scale_fp8_kernel<128, true>,
+                                    (const void*)slab_scale_fp8_kernel<64, false>,
+                                    (const void*)slab_scale_fp8_kernel<64, true>};
+  const void* fs = scale_fns[kix];
   e = hipLaunchKernel(fs, dim3((unsigned)(heads * chunks)), dim3(QTHREADS), qargs, 0, s);
   if (e != hipSuccess) return QIK_ERR_LAUNCH;
   e = hipLaunchKernel(fq, dim3((unsigned)(heads * chunks)), dim3(QTHREADS), qargs, 0, s);

@@ -183,6 +183,9 @@ class ContiguousKVCache:
         device: torch.device | str = "cuda",
         dtype: torch.dtype = torch.bfloat16,
     ):
+        if dtype not in (torch.bfloat16, torch.float16):
+            # the store and attention kernels read 2-byte K/V elements
+            raise ValueError(f"slab dtype must be bfloat16 or float16, got {dtype}")
         self.v_fp8 = v_fp8
         self.num_layers = num_layers
         self.capacity = prefix_max

@@ -249,7 +249,6 @@ def _store_args(**kw):
     (dict(abi_version=0), -2), (dict(dtype=9), -3), (dict(D=32), -4), (dict(P=-1), -5),
     (dict(v_scale=None), -7),                     # fp8 V needs the scale output
     (dict(v_fp8=0), -7),                          # a scale output without fp8 V
-    (dict(dtype=_lib.DTYPE_FP16), -7),            # fp8 V only from bf16 (triton_attention.py:159)
     (dict(k=None), -1), (dict(v_dst=0x10004), -8), (dict(stride_k=_lib._i64x3(8192, 260, 128)), -8),
     (dict(length_dst=0x10004), -8),               # the length is an int64
 ])
@@ -263,7 +262,7 @@ def test_slab_store_without_rows_is_a_no_op():
 
 @pytest.mark.parametrize("kw,code", [
     (dict(abi_version=0), -2), (dict(dtype=9), -3), (dict(D=32), -4), (dict(P=-1), -5),
-    (dict(v_scale=None), -7), (dict(dtype=_lib.DTYPE_FP16), -7),
+    (dict(v_scale=None), -7), (dict(v_fp8=0), -7),
     (dict(k=None), -1), (dict(v_dst=0x10004), -8),
 ])
 def test_slab_store_ws_rejects_like_the_three_launch_store(kw, code):
@@ -423,3 +422,19 @@ def test_fp8_dequant_rejects_before_any_launch():
     assert lib.qik_fp8_dequant(None, 0x20000, 0x30000, 64, _lib.DTYPE_BF16, None) == -1
     assert lib.qik_fp8_dequant(0x10004, 0x20000, 0x30000, 64, _lib.DTYPE_BF16, None) == -8
     assert lib.qik_fp8_dequant(0x10000, 0x20000, 0x30008, 64, _lib.DTYPE_BF16, None) == -8
+
+
+def test_slab_store_fp8_takes_fp16_and_cache_rejects_other_dtypes():
+    """An fp8 slab store validates for an fp16 source as for bf16 (the
+    reference quantises any dtype, kv_cache.py:36-42); the cache refuses
+    element types its kernels cannot read (4-byte fp32, 1-byte) up front."""
+    import torch
+    import qwen_image_kernel_amd as qik
+    lib = _lib.load()
+    for dt in (_lib.DTYPE_BF16, _lib.DTYPE_FP16):
+        n = ctypes.c_int64(-1)
+        assert lib.qik_slab_store_workspace_size(ctypes.byref(_store_args(dtype=dt)), ctypes.byref(n)) == 0
+        assert n.value == 2 * 64 * 4                  # B*H heads x 64 chunk scales
+    for dt in (torch.float32, torch.float8_e4m3fn, torch.int16):
+        with pytest.raises(ValueError, match="bfloat16 or float16"):
+            qik.ContiguousKVCache(1, 1, 16, 2, 128, device="cpu", dtype=dt)

@@ -202,6 +202,51 @@ def test_slab_store_every_bf16_value_under_many_scales():
     np.testing.assert_array_equal(got, codes)
 
 
+@pytest.mark.parametrize("D", [128, 64])
+def test_slab_store_fp16_source_every_value(D):
+    """An fp8 slab in an fp16 model: the reference quantises whatever dtype V
+    has (kv_cache.py:36-42 takes v.float() first).  Every finite fp16 value,
+    shuffled, in heads whose planted amax runs from the largest fp16 (65504)
+    down to the smallest subnormal (2^-24), plus an all-zero head; codes and
+    scales against the oracle and torch's ops on the device, K bit-exact, and
+    the three-launch form against the workspace form."""
+    _flush(f"case slab store fp16 source D={D}")
+    B, P, H = 2, 160, 5
+    allv = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16).view(np.float16)
+    vals = allv[np.isfinite(allv)].astype(np.float32)
+    rng = np.random.default_rng(23 + D)
+    amaxes = [65504.0, 1.0, 448.0, 2.0 ** -14, 2.0 ** -24, 0.0, 3.0, 1e-3, 1000.0, 0.1]
+    v = np.zeros((B, P, H, D), np.float32)
+    for i, am in enumerate(amaxes):
+        b, h = divmod(i, H)
+        am = np.float32(np.float16(am))
+        sel = vals[np.abs(vals) <= am]
+        head = np.resize(rng.permutation(sel), P * D)
+        head[0] = am
+        v[b, :, h, :] = head.reshape(P, D)
+    vh = torch.from_numpy(v).to(torch.float16).to(DEV)
+    k = torch.from_numpy(v[:, ::-1].copy()).to(torch.float16).to(DEV)
+    caches = [qik.ContiguousKVCache(1, B, P + 8, H, D, v_fp8=True, device=DEV, dtype=torch.float16)
+              for _ in range(2)]
+    caches[0].get_layer(0).store(k, vh)                        # workspace form
+    lib = _lib.load()
+    a3, keep3 = caches[1].get_layer(0).store_args(k, vh, P)
+    assert lib.qik_slab_store(ctypes.byref(a3), torch.cuda.current_stream().cuda_stream) == 0
+    torch.cuda.synchronize()
+    kt, vt, st = _torch_store(k, vh, True)
+    codes, scale = of.quantize_per_head(v)
+    for c in caches:                                           # slab layout [B, H, P, D]
+        got = c.v_buf[0, :, :, :P].contiguous().view(torch.uint8).cpu().numpy()
+        sc = c.v_scale[0].cpu().numpy()
+        np.testing.assert_array_equal(got, codes)
+        np.testing.assert_array_equal(got, vt.view(torch.uint8).cpu().numpy())
+        np.testing.assert_array_equal(sc, scale)
+        np.testing.assert_array_equal(sc, st.cpu().numpy())
+        np.testing.assert_array_equal(_bits(c.k_buf[0, :, :, :P]), _bits(kt))
+    assert scale[1, 0] == np.float32(1e-12)                    # the all-zero head
+    del keep3
+
+
 def test_slab_store_rounding_edges():
     """Quotients on e4m3fn ties and in the subnormal range, an all-zero head
     (scale 1e-12) and the extremes +-amax (codes +-448)."""
