@@ -48,6 +48,21 @@ def _check_rows(name: str, t: torch.Tensor) -> None:
         raise ValueError(f"{name} must be a device tensor (the kernel runs on the GPU)")
 
 
+def _kernel_layout(t: torch.Tensor, base: int = 16) -> torch.Tensor:
+    """``t`` itself when the kernel can read it in place: base address a
+    multiple of ``base`` bytes, b/s/h strides multiples of 8 elements (the
+    copies move 16-byte chunks) and rows that do not overlap.  Otherwise a
+    contiguous copy on the same device, so that every layout the reference's
+    kernel takes (it reads any strides) gives a result here too, at the price
+    of one read and one write of ``t``."""
+    B, S, H, D = t.shape
+    sb, ss, sh, _ = t.stride()
+    if (t.data_ptr() % base == 0 and (B == 1 or sb % 8 == 0) and (H == 1 or sh % 8 == 0)
+            and (S == 1 or (ss % 8 == 0 and ss >= D))):
+        return t
+    return t.clone(memory_format=torch.contiguous_format)
+
+
 def make_args(
     query: torch.Tensor,
     key: torch.Tensor,
@@ -205,14 +220,33 @@ def block_causal_flash_attention(
     # with P == 0 the slab (and its fp8 scale) is never read (HAS_CACHE = P > 0, :250)
     if P == 0:
         cache_k = cache_v = scale = None
+    st = _run(query, key, value, L, kv_bytes, out, cache_k, cache_v, scale, uniform, debug_tiles, split_tail, dev)
+    if st == _ERR_ALIGN:
+        # nothing was launched: a layout the kernel cannot read in place goes
+        # through contiguous copies (the reference's kernel reads any strides)
+        query, key, value = _kernel_layout(query), _kernel_layout(key), _kernel_layout(value)
+        if cache_k is not None:
+            cache_k = _kernel_layout(cache_k)
+            cache_v = _kernel_layout(cache_v, 8 if cache_v.dtype == torch.float8_e4m3fn else 16)
+        st = _run(query, key, value, L, kv_bytes, out, cache_k, cache_v, scale, uniform, debug_tiles, split_tail,
+                  dev)
+    _lib.check(st, "qik_attn_fwd_ws" if split_tail else "qik_attn_fwd")
+    return out
+
+
+_ERR_ALIGN = -8  # QIK_ERR_ALIGN
+
+
+def _run(query, key, value, L, kv_bytes, out, cache_k, cache_v, scale, uniform, debug_tiles, split_tail, dev) -> int:
+    """Argument struct (cached per geometry) and launch; the library's status."""
     args, ws_bytes = _cached_args(query, key, value, L, kv_bytes, out, cache_k, cache_v, scale, uniform,
                                   debug_tiles, split_tail)
+    if args is None:
+        return ws_bytes
     if dev.index is not None and dev.index != torch.cuda.current_device():
         with torch.cuda.device(dev):
-            _launch(args, dev, split_tail, ws_bytes)
-    else:
-        _launch(args, dev, split_tail, ws_bytes)
-    return out
+            return _launch(args, dev, split_tail, ws_bytes)
+    return _launch(args, dev, split_tail, ws_bytes)
 
 
 def _check_aux(name: str, t: torch.Tensor, dev: torch.device) -> None:
@@ -246,9 +280,12 @@ def _cached_args(query, key, value, L, kv_bytes, out, cache_k, cache_v, scale, u
     hit = _ARGS_CACHE.get(gkey)
     if hit is None:
         a = make_args(query, key, value, L, kv_bytes, out, cache_k, cache_v, scale, uniform, debug)
+        lib = _lib.load()
+        st = lib.qik_attn_validate(ctypes.byref(a))
+        if st != 0:
+            return None, st   # (None, status): not cached, nothing launched
         ws_bytes = 0
         if split_tail:
-            lib = _lib.load()
             nbytes = ctypes.c_int64(0)
             with torch.cuda.device(query.device):
                 _lib.check(lib.qik_attn_workspace_size(ctypes.byref(a), ctypes.byref(nbytes)),
@@ -310,19 +347,17 @@ def _current_stream(dev: torch.device) -> int:
     return torch._C._cuda_getCurrentRawStream(dev.index if dev.index is not None else torch.cuda.current_device())
 
 
-def _launch(args: _lib.QikAttnArgs, dev: torch.device, split_tail: bool, ws_bytes: int) -> None:
-    """Enqueue the kernel on the current stream of ``dev`` (the current device)."""
+def _launch(args: _lib.QikAttnArgs, dev: torch.device, split_tail: bool, ws_bytes: int) -> int:
+    """Enqueue the kernel on the current stream of ``dev`` (the current device); the status."""
     lib = _lib.load()
     handle = _current_stream(dev)
     stream = ctypes.c_void_p(handle)
     if not split_tail:
-        _lib.check(lib.qik_attn_fwd(ctypes.byref(args), stream), "qik_attn_fwd")
-        return
+        return lib.qik_attn_fwd(ctypes.byref(args), stream)
     ws = None if ws_bytes == 0 else _workspace(dev if dev.index is not None else
                                                torch.device("cuda", torch.cuda.current_device()),
                                                handle, ws_bytes)
-    st = lib.qik_attn_fwd_ws(ctypes.byref(args), None if ws is None else ws.data_ptr(), ws_bytes, stream)
-    _lib.check(st, "qik_attn_fwd_ws")
+    return lib.qik_attn_fwd_ws(ctypes.byref(args), None if ws is None else ws.data_ptr(), ws_bytes, stream)
 
 
 def _norm_slice(start: int, stop: int | None, n: int) -> tuple[int, int]:

@@ -59,7 +59,7 @@ def fused_rms_norm_rope(
     # checked and prepared once per key -- the argument struct with the
     # weight and cos/sin pointers filled in, the output shape.  Only x's and
     # the output's data pointers change between calls.
-    key = (x.shape, x.stride(), x.dtype, x.device, eps,
+    key = (x.shape, x.stride(), x.data_ptr() & 15, x.dtype, x.device, eps,
            weight.data_ptr(), weight._version, weight.dtype, weight.shape, weight.stride(), weight.device,
            freqs_cis.data_ptr(), freqs_cis._version, freqs_cis.dtype, freqs_cis.shape, freqs_cis.stride(),
            freqs_cis.device)
@@ -70,7 +70,7 @@ def fused_rms_norm_rope(
             _CALLS.clear()
         _CALLS[key] = ent
     if ent.contig:
-        x = x.contiguous()
+        x = x.clone(memory_format=torch.contiguous_format)
     out = x.new_empty(ent.shape)
     a = _lib.QikRmsRopeArgs.from_buffer_copy(ent.args)
     a.x = x.data_ptr()
@@ -107,8 +107,14 @@ def _prepare(x, weight, freqs_cis, eps) -> _Call:
     B, S, H, D = x.shape
     if tuple(freqs_cis.shape) != (S, D // 2):
         raise ValueError(f"freqs_cis must be [S, D/2] = {(S, D // 2)}, got {tuple(freqs_cis.shape)}")
-    contig = D > 1 and x.stride(-1) != 1
-    xs = x.contiguous() if contig else x
+    # the kernel reads 16-byte chunks in place from a 16-byte aligned base with
+    # b/s/h strides in multiples of 8 elements and a unit D stride; any other
+    # layout (the reference's kernel reads any strides) goes through a
+    # contiguous copy made at each call
+    sb, ss, sh, sd = x.stride()
+    contig = ((D > 1 and sd != 1) or x.data_ptr() % 16 != 0 or (B > 1 and sb % 8 != 0)
+              or (S > 1 and ss % 8 != 0) or (H > 1 and sh % 8 != 0))
+    xs = x.clone(memory_format=torch.contiguous_format) if contig else x
     w = weight
     if w.dtype != torch.float32 or w.device != x.device or not w.is_contiguous():
         w = weight.to(device=x.device, dtype=torch.float32).contiguous()

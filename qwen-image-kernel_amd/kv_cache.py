@@ -27,6 +27,7 @@ import ctypes
 import torch
 
 from . import _lib
+from .attention import _kernel_layout
 
 FP8_E4M3_MAX = 448.0
 
@@ -65,6 +66,13 @@ class _LayerView:
     def _store_device(self, k: torch.Tensor, v: torch.Tensor, P: int) -> None:
         c = self._c
         kd = c.k_buf
+        # inputs the kernels cannot read in place (a base off 16 bytes, odd
+        # strides) go through contiguous copies; other dtypes or devices are
+        # converted (into fresh tensors) by store_args
+        if k.dim() == 4 and k.device == kd.device and k.dtype == kd.dtype:
+            k = _kernel_layout(k)
+        if v.dim() == 4 and v.device == kd.device and v.dtype == kd.dtype:
+            v = _kernel_layout(v)
         a, keep, nbytes = self._cached_store_args(k, v, P)
         lib = _lib.load()
         idx = kd.device.index

@@ -312,13 +312,23 @@ def test_deterministic():
     assert torch.equal(a, b)
 
 
-def test_misaligned_input_is_rejected():
+def test_misaligned_input_rejected_by_the_abi_and_copied_by_the_wrapper():
+    """A base 8 bytes off 16-byte alignment: qik_attn_validate rejects it
+    (QIK_ERR_ALIGN, before any launch); the Python entry point runs it through
+    a contiguous copy and returns the bits of the call on aligned inputs."""
+    import ctypes
+    from qwen_image_kernel_amd import _lib, attention
     g = torch.Generator().manual_seed(960)
     base = _rand((64 * 4 * 128 + 4,), g).to(DEV)
     q = base[4:].view(1, 64, 4, 128)                 # 8-byte offset: not 16-byte aligned
     L = torch.arange(64, dtype=torch.int32, device=DEV)
-    with pytest.raises(RuntimeError, match="QIK_ERR_ALIGN"):
-        qik.block_causal_flash_attention(q, q, q, L, None)
+    out = torch.empty(q.shape, dtype=q.dtype, device=DEV)
+    a = attention.make_args(q, q, q, L, None, out, None, None, None, False)
+    assert _lib.load().qik_attn_validate(ctypes.byref(a)) == -8
+    got = qik.block_causal_flash_attention(q, q, q, L, None)
+    qc = q.clone()
+    want = qik.block_causal_flash_attention(qc, qc, qc, L, None)
+    np.testing.assert_array_equal(got.view(torch.int16).cpu().numpy(), want.view(torch.int16).cpu().numpy())
 
 
 def test_side_inputs_on_the_host_or_misshaped_are_rejected():
