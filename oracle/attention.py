@@ -74,14 +74,19 @@ def attention_fp32(query, key, value, prefix_lengths, key_valid=None, cache_k=No
     for b in (range(B) if batches is None else batches):
         al = allowed if kvm is None else (allowed & kvm[b][None, :KV])
         any_row = al.any(dim=1, keepdim=True)
+        # with every key allowed (uniform lengths) the mask and the empty-row
+        # guard change nothing and are skipped
+        full = bool(al.all())
         for h in (range(H) if heads is None else heads):
             qt = torch.from_numpy(np.ascontiguousarray(q[b, :, h]))
             kt = torch.from_numpy(np.ascontiguousarray(k[b, :, h]))
             vt = torch.from_numpy(np.ascontiguousarray(v[b, :, h]))
             s = (qt @ kt.T) * scale
-            s = s.masked_fill(~al, float("-inf"))
+            if not full:
+                s = s.masked_fill(~al, float("-inf"))
             p = torch.softmax(s, dim=-1)
-            p = torch.where(any_row, p, torch.zeros_like(p))
+            if not full:
+                p = torch.where(any_row, p, torch.zeros_like(p))
             out[b, :, h] = (p @ vt).numpy()
     return out
 

@@ -424,10 +424,12 @@ def _wl_run(wl, inp):
                                             cache_v_scale=inp["cache_v_scale"], uniform_full=wl.uniform)
 
 
-@pytest.mark.parametrize("name,heads", [("tiny", None), ("t2i_512", None), ("t2i_1024", [0, 23]),
-                                        ("edit_768", [0, 11]), ("multiref_cfg", [5])])
+@pytest.mark.parametrize("name,heads", [("tiny", None), ("t2i_512", None), ("t2i_1024", None),
+                                        ("edit_768", None), ("multiref_cfg", [0, 5, 17, 23])])
 def test_benchmark_shapes_vs_oracle(name, heads):
-    """CPU oracle on the same seeded inputs (all heads for the small shapes, a few for the big ones)."""
+    """CPU oracle on the same seeded inputs: every head of every shape up to the
+    two headline ones (t2i_1024 and edit_768, 24 heads each), four heads of the
+    last batch of multiref_cfg."""
     _flush(f"case shape {name}")
     wl = wls.workload(name)
     inp = wls.make_inputs(wl, seed=1000 * (wls.NAMES.index(name) + 1), device=DEV)
