@@ -438,3 +438,24 @@ def test_slab_store_fp8_takes_fp16_and_cache_rejects_other_dtypes():
     for dt in (torch.float32, torch.float8_e4m3fn, torch.int16):
         with pytest.raises(ValueError, match="bfloat16 or float16"):
             qik.ContiguousKVCache(1, 1, 16, 2, 128, device="cpu", dtype=dt)
+
+
+def test_kernel_layout_rule():
+    """The wrappers' layout rule on host tensors: a fused-QKV slice (strides
+    multiples of 8, 16-byte base) is passed through in place; an offset base, a
+    row stride off a multiple of 8 and overlapping rows get a contiguous copy
+    with a 16-byte aligned base and the same values."""
+    import torch
+    qkv = torch.randn(2, 40, 3 * 4 * 128).to(torch.bfloat16)
+    q = qkv.unflatten(-1, (12, 128))[:, :, :4]
+    assert attention._kernel_layout(q) is q
+    buf = torch.randn(2 * 40 * 4 * 128 + 3).to(torch.bfloat16)
+    odd_base = buf[3:].view(2, 40, 4, 128)
+    odd_row = torch.randn(2, 40, 4, 132).to(torch.bfloat16)[..., :128]
+    overlap = torch.randn(2, 1, 4, 128).to(torch.bfloat16).expand(2, 40, 4, 128)
+    for t in (odd_base, odd_row, overlap):
+        c = attention._kernel_layout(t)
+        assert c is not t and c.is_contiguous() and c.data_ptr() % 16 == 0
+        assert torch.equal(c, t)
+    fp8 = torch.zeros(1, 16, 2, 128, dtype=torch.float8_e4m3fn)
+    assert attention._kernel_layout(fp8, 8) is fp8
