@@ -9,6 +9,9 @@
  *                     (the `torch._scaled_mm` call, fp8.py:87-88)
  *   qik_fp8_dequant   bf16(fp32(w_fp8) * scale), the weight of the bf16 path
  *                     that layers with fewer than 256 inputs take (fp8.py:79-84)
+ *   qik_fp8_quantize_weight_host
+ *                     the weight quantiser for a weight in host memory, run on
+ *                     the CPU (`quantize_weight_tensorwise` of a CPU tensor)
  *
  * Same conventions as qik_attn.h: plain C, no allocation, device pointers of
  * the current HIP device, `stream` a hipStream_t as void*, asynchronous and
@@ -111,10 +114,28 @@ int qik_fp8_gemm(const qik_fp8_gemm_args* args, void* stream);
 int qik_fp8_gemm_workspace_size(const qik_fp8_gemm_args* args, int64_t* bytes);
 int qik_fp8_gemm_ws(const qik_fp8_gemm_args* args, void* workspace, int64_t workspace_bytes, void* stream);
 
-/* out[i] = round(fp32(code[i]) * scale[0]) into out_dtype (bf16 or fp16), for
- * i < n: the dequantised weight of the bf16 path (fp8.py:81: fp8 -> bf16 ->
- * fp32 is exact, one fp32 multiply, one round).  w 8-byte aligned, out 16. */
+/* out[i] = round(fp32(code[i]) * scale[0]) into out_dtype, for i < n: the
+ * dequantised weight of the bf16 path (fp8.py:81: fp8 -> bf16 -> fp32 is
+ * exact, one fp32 multiply).  out_dtype QIK_DTYPE_BF16 or QIK_DTYPE_FP16
+ * rounds once to nearest even; QIK_DTYPE_FP32 writes the fp32 product itself
+ * (the weight an fp32 activation multiplies, fp8.py:81-82).  w 8-byte
+ * aligned, out 16. */
 int qik_fp8_dequant(const void* w, const float* scale, void* out, int64_t n, int32_t out_dtype, void* stream);
+
+/* Weight quantisation of a weight in HOST memory, on the CPU (no device
+ * involved): replaces `quantize_weight_tensorwise` (fp8.py:56-60) when the
+ * weight is a CPU tensor, as in the offline conversion on a machine without
+ * a GPU (quantize_offline.py:15-25).  Bit-identical to those torch ops run on
+ * the CPU, where both divisions are IEEE fp32 divisions:
+ *   scale = max(amax / 448, 1e-12)                    (NaN stays NaN)
+ *   out   = e4m3fn_rne(clamp(fp32(w) / scale, +-448))
+ * (qik_fp8_quantize's QIK_FP8_WEIGHT mode gives what the same ops give on a
+ * HIP device, where torch multiplies the amax by the reciprocal of 448.)
+ * w: n host elements of `dtype` (QIK_DTYPE_BF16, _FP16 or _FP32); out: n host
+ * bytes; *scale written.  `threads` host threads at most (< 1 means 1); the
+ * bytes do not depend on it.  Blocking; 1 <= n < 2^40. */
+int qik_fp8_quantize_weight_host(const void* w, int32_t dtype, int64_t n, void* out, float* scale,
+                                 int32_t threads);
 
 #ifdef __cplusplus
 }

@@ -237,6 +237,8 @@ EXPORTS = (
      (ctypes.POINTER(QikFp8GemmArgs), ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p)),
     ("qik_fp8_dequant", ctypes.c_int,
      (ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p)),
+    ("qik_fp8_quantize_weight_host", ctypes.c_int,
+     (ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32)),
 )
 
 _lock = threading.Lock()

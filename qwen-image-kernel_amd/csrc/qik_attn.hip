@@ -235,17 +235,25 @@ __device__ __forceinline__ void g_store(unsigned* p, unsigned v) {
 // k-th barrier waiting for 4k arrivals.  The caller has waited for its tile
 // copies; the release fence waits for its LDS writes.  The spin is bounded
 // (2^18 polls of at least 64 cycles, milliseconds beyond any real wait), so no
-// mistake can hold the device.
-__device__ __forceinline__ void group_sync(int* ctr, int& target, int lane) {
+// mistake can hold the device; it returns false when the bound ran out, and
+// the kernel then writes NaN into the row block's output (the tiles read
+// after such a barrier may be half-written), so a tripped bound shows as an
+// error, never as plausible numbers.
+__device__ __forceinline__ bool group_sync(int* ctr, int& target, int lane) {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   if (lane == 0) __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   target += 4;
+  bool reached = false;
   for (int i = 0; i < (1 << 18); ++i) {
     const int seen = __builtin_amdgcn_readfirstlane(__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
-    if (seen >= target) break;
+    if (seen >= target) {
+      reached = true;
+      break;
+    }
     __builtin_amdgcn_s_sleep(1);
   }
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  return reached;
 }
 
 // Wave-wide min or max of an int, returned as a wave-uniform value: four DPP
@@ -364,13 +372,14 @@ __global__ void __launch_bounds__(NTHREADS * KSPLIT, KSPLIT == 1 ? 2 : 1) attn_f
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   if (KSPLIT == 2 && tid == 0) gctr[grp] = 0;  // read only after the first full barrier
   int gtarget = 0;
+  bool synced = true;  // two-group kernel: every group barrier of this unit completed
   // the barrier between tiles: the workgroup's, or the group's own in the
   // two-group kernel (the groups then run free, as two workgroups would)
   auto tile_sync = [&]() {
     if constexpr (KSPLIT == 1) {
       __syncthreads();
     } else {
-      group_sync(&gctr[grp], gtarget, lane);
+      synced = group_sync(&gctr[grp], gtarget, lane) && synced;
     }
   };
   const int hf = lane >> 5;   // lane half: keys 4*hf.. of each 8-key group
@@ -807,7 +816,8 @@ __global__ void __launch_bounds__(NTHREADS * KSPLIT, KSPLIT == 1 ? 2 : 1) attn_f
             for (int q4 = 0; q4 < 4; ++q4)
               xs[(db * 4 + q4) * NTHREADS + tid] =
                   f32x4{oacc[db][4 * q4 + 0], oacc[db][4 * q4 + 1], oacc[db][4 * q4 + 2], oacc[db][4 * q4 + 3]};
-          sml[tid] = f32x2{m_run, l_run};
+          // a timed-out group barrier poisons the merged row sums
+          sml[tid] = f32x2{m_run, synced ? l_run : __builtin_nanf("")};
         }
         __syncthreads();
         if (grp == 0) {
@@ -902,8 +912,12 @@ __global__ void __launch_bounds__(NTHREADS * KSPLIT, KSPLIT == 1 ? 2 : 1) attn_f
     // behind the draw's barriers), read back as whole rows, so that a store
     // instruction writes 1 KiB of whole rows instead of 16 B into each of 32
     // rows (which took ~2 us per unit, measured).  Rows past SQ are not stored.
+    if constexpr (KSPLIT == 2) {
+      if (!synced) l_part = __builtin_nanf("");
+    }
     const float l_tot = pair_sum(l_part);
-    const float inv = (l_tot > 0.0f) ? 1.0f / l_tot : 0.0f;
+    // a NaN row sum (non-finite inputs, or a timed-out group barrier) gives NaN rows
+    const float inv = (l_tot > 0.0f) ? 1.0f / l_tot : (l_tot == l_tot ? 0.0f : l_tot);
     if (pulled && tid == 0) snext = gx + (int)pend;
     if constexpr (V_FP8 || KV) {
       // kernels that write LDS inside the tile loop (the fp8 V dequantisation,

@@ -27,6 +27,9 @@
 #include <string.h>
 #include <limits.h>
 #include <algorithm>
+#include <cmath>
+#include <thread>
+#include <vector>
 
 #include "qik_fp8.h"
 
@@ -289,32 +292,48 @@ __device__ __forceinline__ f32x2 decode2(unsigned w) {
   return __builtin_amdgcn_cvt_pk_f32_fp8((int)w, HI);
 }
 
-template <bool FP16>
+// round(fp32(code) * s) in the output type (OUT: QIK_DTYPE_BF16, _FP16 or
+// _FP32, the last with no rounding: the exact fp32 product)
+template <int OUT>
+__device__ __forceinline__ void dequant_store(f32x2 f, float s, char* out, int64_t pair) {
+#pragma clang fp contract(off)
+  f[0] *= s;
+  f[1] *= s;
+  // the empty asm keeps the fp32 product from being folded into a
+  // mixed-precision fma that rounds once
+  asm volatile("" : "+v"(f));
+  if constexpr (OUT == QIK_DTYPE_FP32) {
+    reinterpret_cast<f32x2*>(out)[pair] = f;
+  } else {
+    reinterpret_cast<unsigned*>(out)[pair] = pack2<OUT == QIK_DTYPE_FP16>(f[0], f[1]);
+  }
+}
+
+template <int OUT>
 __global__ void __launch_bounds__(QT) dequant_kernel(const unsigned char* w, const float* scale, char* out,
                                                       int64_t n) {
-#pragma clang fp contract(off)
   const float s = scale[0];
   const int64_t v = (int64_t)blockIdx.x * QT + threadIdx.x;  // 8 codes per thread
   const int64_t nvec = n / 8;
   if (v < nvec) {
     const u32x2 c = reinterpret_cast<const u32x2*>(w)[v];
-    u32x4 o;
-    f32x2 f;
-    // round(fp32(code) * s) in the output type; the empty asm keeps the fp32
-    // product from being folded into a mixed-precision fma that rounds once
-    f = decode2<false>(c.x); f[0] *= s; f[1] *= s; asm volatile("" : "+v"(f)); o.x = pack2<FP16>(f[0], f[1]);
-    f = decode2<true>(c.x);  f[0] *= s; f[1] *= s; asm volatile("" : "+v"(f)); o.y = pack2<FP16>(f[0], f[1]);
-    f = decode2<false>(c.y); f[0] *= s; f[1] *= s; asm volatile("" : "+v"(f)); o.z = pack2<FP16>(f[0], f[1]);
-    f = decode2<true>(c.y);  f[0] *= s; f[1] *= s; asm volatile("" : "+v"(f)); o.w = pack2<FP16>(f[0], f[1]);
-    reinterpret_cast<u32x4*>(out)[v] = o;
+    dequant_store<OUT>(decode2<false>(c.x), s, out, 4 * v + 0);
+    dequant_store<OUT>(decode2<true>(c.x), s, out, 4 * v + 1);
+    dequant_store<OUT>(decode2<false>(c.y), s, out, 4 * v + 2);
+    dequant_store<OUT>(decode2<true>(c.y), s, out, 4 * v + 3);
   }
   if (v == 0) {
     for (int64_t i = nvec * 8; i < n; ++i) {
+#pragma clang fp contract(off)
       f32x2 f = decode2<false>((unsigned)w[i]);
       f[0] *= s;
       asm volatile("" : "+v"(f));
-      const unsigned h = pack2<FP16>(f[0], 0.0f);
-      reinterpret_cast<unsigned short*>(out)[i] = (unsigned short)(h & 0xffffu);
+      if constexpr (OUT == QIK_DTYPE_FP32) {
+        reinterpret_cast<float*>(out)[i] = f[0];
+      } else {
+        const unsigned h = pack2<OUT == QIK_DTYPE_FP16>(f[0], 0.0f);
+        reinterpret_cast<unsigned short*>(out)[i] = (unsigned short)(h & 0xffffu);
+      }
     }
   }
 }
@@ -928,6 +947,115 @@ int launch_gemm(GemmParams& p, const qik_fp8_gemm_args* a, int64_t n1, bool fp16
   return hipLaunchKernel(fn, dim3(grid), dim3(C1::NT), args, 0, s) == hipSuccess ? QIK_OK : QIK_ERR_LAUNCH;
 }
 
+// ---------------------------------------------------------------------------
+// Weight quantiser for weights in host memory (no device involved)
+// ---------------------------------------------------------------------------
+//
+// What torch's CPU ops compute for (w.abs().amax().float() / 448).clamp_min(1e-12)
+// and (w.float() / scale).clamp(-448, 448).to(float8_e4m3fn) (fp8.py:56-60):
+// on the CPU both divisions are IEEE fp32 divisions (on a HIP device torch
+// multiplies by the fp32 reciprocal of 448 instead, which is what the device
+// quantiser reproduces).  Elementwise, so any thread split gives the same
+// bytes.
+
+// exact fp32 value of element i of a bf16 / fp16 / fp32 host array
+inline float host_elem(const void* w, int32_t dtype, int64_t i) {
+  if (dtype == QIK_DTYPE_FP32) return static_cast<const float*>(w)[i];
+  const uint16_t h = static_cast<const uint16_t*>(w)[i];
+  uint32_t bits;
+  if (dtype == QIK_DTYPE_BF16) {
+    bits = (uint32_t)h << 16;
+  } else {
+    // binary16: 1 sign, 5 exponent bits (bias 15), 10 mantissa bits
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    const uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+    if (e == 0x1f) {
+      bits = sign | 0x7f800000u | (m << 13);
+    } else if (e != 0) {
+      bits = sign | ((e + 112u) << 23) | (m << 13);
+    } else {
+      // zero or subnormal: m * 2^-24, exact in fp32
+      const float f = (float)m * 5.9604644775390625e-8f;
+      memcpy(&bits, &f, 4);
+      bits |= sign;
+    }
+  }
+  float f;
+  memcpy(&f, &bits, 4);
+  return f;
+}
+
+// e4m3fn code of q (|q| <= 448 or NaN), round to nearest even; NaN keeps its
+// sign bit (0x7f / 0xff), and a magnitude that rounds past 448 is NaN (the
+// format has no infinity)
+inline unsigned char host_e4m3fn(float q) {
+  uint32_t u;
+  memcpy(&u, &q, 4);
+  const unsigned char sign = (unsigned char)((u >> 24) & 0x80u);
+  const uint32_t a = u & 0x7fffffffu;
+  if (a >= 0x43e80000u) return sign | 0x7f;  // NaN, or |q| >= 464 (= 448 + half a step)
+  if (a < 0x3c800000u) {
+    // below 2^-6: subnormal codes m * 2^-9, m = round_even(|q| * 512) (exact scaling)
+    float fa;
+    memcpy(&fa, &a, 4);
+    return sign | (unsigned char)std::nearbyint(fa * 512.0f);
+  }
+  // normal: keep 3 mantissa bits with round-to-nearest-even at bit 20, then
+  // move the exponent from bias 127 to bias 7
+  const uint32_t r = a + 0x7ffffu + ((a >> 20) & 1u);
+  return sign | (unsigned char)((r >> 20) - (120u << 3));
+}
+
+int host_quantize_weight(const void* w, int32_t dtype, int64_t n, unsigned char* out, float* scale_out,
+                         int32_t threads) {
+  const int nt = (int)std::max<int64_t>(1, std::min<int64_t>(std::max(threads, 1), (n + 65535) / 65536));
+  auto chunk = [&](int t, int64_t& i0, int64_t& i1) {
+    i0 = n * t / nt;
+    i1 = n * (t + 1) / nt;
+  };
+  // amax as fp32 bit patterns of |x|: unsigned order is |x| order with NaN
+  // above +inf, so a NaN anywhere gives a NaN amax, as torch's amax does
+  std::vector<uint32_t> part(nt, 0u);
+  auto amax_part = [&](int t) {
+    int64_t i0, i1;
+    chunk(t, i0, i1);
+    uint32_t m = 0;
+    for (int64_t i = i0; i < i1; ++i) {
+      uint32_t b;
+      const float f = host_elem(w, dtype, i);
+      memcpy(&b, &f, 4);
+      m = std::max(m, b & 0x7fffffffu);
+    }
+    part[t] = m;
+  };
+  std::vector<std::thread> pool;
+  for (int t = 1; t < nt; ++t) pool.emplace_back(amax_part, t);
+  amax_part(0);
+  for (auto& th : pool) th.join();
+  pool.clear();
+  uint32_t mb = 0;
+  for (uint32_t v : part) mb = std::max(mb, v);
+  float amax;
+  memcpy(&amax, &mb, 4);
+  volatile float d448 = 448.0f;  // a division, not a multiply by a folded reciprocal
+  float scale = amax / d448;
+  if (!(scale != scale)) scale = std::max(scale, 1e-12f);
+  *scale_out = scale;
+  auto codes = [&](int t) {
+    int64_t i0, i1;
+    chunk(t, i0, i1);
+    for (int64_t i = i0; i < i1; ++i) {
+      float q = host_elem(w, dtype, i) / scale;
+      if (q == q) q = std::min(std::max(q, -448.0f), 448.0f);
+      out[i] = host_e4m3fn(q);
+    }
+  };
+  for (int t = 1; t < nt; ++t) pool.emplace_back(codes, t);
+  codes(0);
+  for (auto& th : pool) th.join();
+  return QIK_OK;
+}
+
 }  // namespace qik_fp8
 
 extern "C" {
@@ -1049,7 +1177,8 @@ int qik_fp8_gemm_ws(const qik_fp8_gemm_args* a, void* workspace, int64_t workspa
 
 int qik_fp8_dequant(const void* w, const float* scale, void* out, int64_t n, int32_t out_dtype, void* stream) {
   using namespace qik_fp8;
-  if (out_dtype != QIK_DTYPE_BF16 && out_dtype != QIK_DTYPE_FP16) return QIK_ERR_DTYPE;
+  if (out_dtype != QIK_DTYPE_BF16 && out_dtype != QIK_DTYPE_FP16 && out_dtype != QIK_DTYPE_FP32)
+    return QIK_ERR_DTYPE;
   if (n < 0 || n / 8 >= (int64_t)INT_MAX * QT) return QIK_ERR_SHAPE;
   if (n == 0) return QIK_OK;
   if (w == nullptr || scale == nullptr || out == nullptr) return QIK_ERR_NULL_ARG;
@@ -1058,11 +1187,22 @@ int qik_fp8_dequant(const void* w, const float* scale, void* out, int64_t n, int
   const unsigned char* wp = static_cast<const unsigned char*>(w);
   char* op = static_cast<char*>(out);
   void* args[] = {&wp, &scale, &op, &n};
-  const void* fn = out_dtype == QIK_DTYPE_FP16 ? (const void*)dequant_kernel<true> : (const void*)dequant_kernel<false>;
+  const void* fn = out_dtype == QIK_DTYPE_FP16   ? (const void*)dequant_kernel<QIK_DTYPE_FP16>
+                   : out_dtype == QIK_DTYPE_FP32 ? (const void*)dequant_kernel<QIK_DTYPE_FP32>
+                                                 : (const void*)dequant_kernel<QIK_DTYPE_BF16>;
   return hipLaunchKernel(fn, dim3((unsigned)grid), dim3(QT), args, 0, static_cast<hipStream_t>(stream)) ==
                  hipSuccess
              ? QIK_OK
              : QIK_ERR_LAUNCH;
+}
+
+int qik_fp8_quantize_weight_host(const void* w, int32_t dtype, int64_t n, void* out, float* scale,
+                                 int32_t threads) {
+  using namespace qik_fp8;
+  if (dtype != QIK_DTYPE_BF16 && dtype != QIK_DTYPE_FP16 && dtype != QIK_DTYPE_FP32) return QIK_ERR_DTYPE;
+  if (n < 1 || n >= ((int64_t)1 << 40)) return QIK_ERR_SHAPE;
+  if (w == nullptr || out == nullptr || scale == nullptr) return QIK_ERR_NULL_ARG;
+  return host_quantize_weight(w, dtype, n, static_cast<unsigned char*>(out), scale, threads);
 }
 
 }  // extern "C"

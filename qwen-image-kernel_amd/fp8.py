@@ -18,15 +18,23 @@ include/qik_fp8.h, asynchronously on the current stream:
   weight is dequantised by ``qik_fp8_dequant`` and multiplied by
   ``torch.nn.functional.linear``, as in the reference.
 
-Weights that live on the CPU are quantised on the current HIP device and the
-result is moved back (the reference's offline builder does the same,
-quantize_offline.py:19-26); the scale is therefore always the one torch forms
-on a GPU (the amax times the fp32 reciprocal of 448).
+A weight that lives on the CPU is quantised on the CPU by the library's host
+routine ``qik_fp8_quantize_weight_host``, bit-identical to the reference's
+torch ops run on the CPU (where both divisions are true fp32 divisions), so the
+offline conversion runs on a machine without a GPU as the reference's does
+(quantize_offline.py:15-25).  A weight on a HIP device gets the scale torch
+forms there (the amax times the fp32 reciprocal of 448).
+
+``FP8Linear`` keeps a small per-module cache of prepared launch arguments.  It
+holds no tensor (weak references only), is dropped by ``.to()``/``.cuda()``/
+``.half()`` and by copying or pickling the module, so the module moves,
+copies and frees its buffers exactly as the reference's does.
 """
 
 from __future__ import annotations
 
 import ctypes
+import weakref
 
 import torch
 import torch.nn as nn
@@ -48,6 +56,8 @@ FP8_E4M3_MAX = 448.0
 
 _IN_DTYPES = {torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_FP16, torch.float32: _lib.DTYPE_FP32}
 _OUT_DTYPES = {torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_FP16}
+# element types qik_fp8_dequant writes
+_DEQUANT_DTYPES = _IN_DTYPES
 
 # partial-maximum workspace of the quantiser, one per (device, stream); the
 # kernels write every word they read, so it is never cleared
@@ -60,6 +70,11 @@ def _stream(dev: torch.device) -> int:
 
 
 def _quant_workspace(dev: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+    """Partial-maximum workspace of the quantiser on this stream.  Under graph
+    capture a fresh one from the graph's pool, so that replays of different
+    graphs (or a replay beside eager work) never share one."""
+    if torch.cuda.is_current_stream_capturing():
+        return torch.empty(max(nbytes // 4, 1024), dtype=torch.int32, device=dev)
     key = (dev.index, stream)
     ws = _QUANT_WS.get(key)
     if ws is None or ws.numel() * 4 < nbytes:
@@ -69,19 +84,23 @@ def _quant_workspace(dev: torch.device, stream: int, nbytes: int) -> torch.Tenso
     return ws
 
 
-def _gemm_workspace(dev: torch.device, stream: int, nbytes: int) -> int:
-    """Address of a workspace of at least nbytes for qik_fp8_gemm_ws on this
-    stream (0 when the call needs none).  One per (device, stream), grown as
-    needed: calls on one stream run in order, so they can share it."""
+def _gemm_workspace(dev: torch.device, stream: int, nbytes: int) -> torch.Tensor | None:
+    """A workspace of at least nbytes for qik_fp8_gemm_ws on this stream
+    (None when the call needs none).  One per (device, stream), grown as
+    needed: calls on one stream run in order, so they can share it.  Under
+    graph capture a fresh one from the graph's pool (the split-K sums of two
+    graphs replayed on different streams must not share memory)."""
     if nbytes <= 0:
-        return 0
+        return None
+    if torch.cuda.is_current_stream_capturing():
+        return torch.empty((nbytes + 3) // 4, dtype=torch.float32, device=dev)
     key = (dev.index, stream)
     ws = _GEMM_WS.get(key)
     if ws is None or ws.numel() * 4 < nbytes:
         if len(_GEMM_WS) >= 64:
             _GEMM_WS.clear()
         ws = _GEMM_WS[key] = torch.empty((nbytes + 3) // 4, dtype=torch.float32, device=dev)
-    return ws.data_ptr()
+    return ws
 
 
 def quant_args(flat: torch.Tensor, out: torch.Tensor, scale: torch.Tensor, mode: int) -> _lib.QikFp8QuantArgs:
@@ -135,27 +154,42 @@ def quantize_tensorwise(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
 def quantize_weight_tensorwise(w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """[N, K] -> (fp8 codes e4m3(clamp(w / scale, +-448)), scale [1]) (fp8.py:56-60).
 
-    A CPU tensor is quantised on the current HIP device and the results come
-    back to the CPU."""
+    On a HIP device: the device quantiser.  A CPU tensor is quantised on the
+    CPU by the library's host routine, with the results torch's CPU ops give
+    (the reference's offline conversion runs there, quantize_offline.py:15-25)."""
     if w.is_cuda:
         return _quantize(w, _lib.FP8_WEIGHT)
-    if not torch.cuda.is_available():
-        raise RuntimeError("quantize_weight_tensorwise needs a HIP device (the quantiser is a GPU kernel)")
-    wq, s = _quantize(w.to(torch.device("cuda", torch.cuda.current_device())), _lib.FP8_WEIGHT)
-    return wq.to(w.device), s.to(w.device)
+    if w.device.type != "cpu":
+        raise ValueError(f"quantize_weight_tensorwise takes a HIP or CPU tensor, got {w.device}")
+    if w.dtype not in _IN_DTYPES:
+        raise ValueError(f"quantiser input must be bf16, fp16 or fp32, got {w.dtype}")
+    if w.numel() == 0:
+        raise ValueError("cannot quantise an empty tensor (its amax is undefined)")
+    wc = w.contiguous()
+    codes = torch.empty(w.shape, dtype=torch.float8_e4m3fn)
+    scale = torch.empty(1, dtype=torch.float32)
+    _lib.check(_lib.load().qik_fp8_quantize_weight_host(wc.data_ptr(), _IN_DTYPES[wc.dtype], wc.numel(),
+                                                        codes.data_ptr(), scale.data_ptr(),
+                                                        torch.get_num_threads()),
+               "qik_fp8_quantize_weight_host")
+    return codes, scale
 
 
 def _dequant_weight(w: torch.Tensor, scale: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
-    """round(fp32(w) * scale) in `dtype` (the bf16 path's weight, fp8.py:81)."""
-    if dtype not in _OUT_DTYPES:
-        dtype = torch.bfloat16
+    """fp32(w) * scale (fp8.py:81) in `dtype` when that is bf16, fp16 or fp32
+    (rounded once, or the fp32 product itself); for any other dtype the fp32
+    product, which the caller converts as the reference's ``w.to(x.dtype)``
+    does."""
+    if not w.is_cuda:
+        raise ValueError("FP8Linear runs on a HIP device; move the module there first")
+    kdt = dtype if dtype in _DEQUANT_DTYPES else torch.float32
     wc = w.contiguous()
-    out = torch.empty(wc.shape, dtype=dtype, device=w.device)
+    out = torch.empty(wc.shape, dtype=kdt, device=w.device)
     sc = scale.to(device=w.device, dtype=torch.float32).contiguous()
     lib = _lib.load()
     with torch.cuda.device(w.device):
         _lib.check(
-            lib.qik_fp8_dequant(wc.data_ptr(), sc.data_ptr(), out.data_ptr(), wc.numel(), _OUT_DTYPES[dtype],
+            lib.qik_fp8_dequant(wc.data_ptr(), sc.data_ptr(), out.data_ptr(), wc.numel(), _DEQUANT_DTYPES[kdt],
                                 _stream(w.device)),
             "qik_fp8_dequant",
         )
@@ -222,25 +256,39 @@ def fp8_linear(
         _lib.check(lib.qik_fp8_gemm_workspace_size(ctypes.byref(a), ctypes.byref(need)), "qik_fp8_gemm")
         stream = _stream(dev)
         ws = _gemm_workspace(dev, stream, need.value)
-        _lib.check(lib.qik_fp8_gemm_ws(ctypes.byref(a), ws or None, need.value, stream), "qik_fp8_gemm")
+        _lib.check(lib.qik_fp8_gemm_ws(ctypes.byref(a), None if ws is None else ws.data_ptr(), need.value, stream),
+                   "qik_fp8_gemm")
     return out
 
 
 class _LinearCall:
-    """What one FP8Linear.forward key (input geometry, weight, scale and bias
-    tensors and their versions) needs at call time."""
+    """What one FP8Linear.forward input geometry needs at call time: the
+    argument structs of the quantise + GEMM pair, and weak references to the
+    weight, scale and bias they were made for (with those tensors' versions),
+    so that the entry is used only while the module still holds exactly them
+    and never keeps them alive."""
 
     __slots__ = ("fast", "index", "xq_shape", "out_shape", "result_shape", "ws_bytes", "gws_bytes", "qargs", "gargs",
-                 "quantize", "gemm", "keep")
+                 "refs", "versions")
+
+    def matches(self, weight, wscale, bias) -> bool:
+        r = self.refs
+        if r[0]() is not weight or r[1]() is not wscale:
+            return False
+        if (r[2] is None) != (bias is None) or (bias is not None and r[2]() is not bias):
+            return False
+        return self.versions == (weight._version, wscale._version, None if bias is None else bias._version)
 
 
 def _prepare_linear(x, weight, wscale, bias, out_features) -> _LinearCall:
-    """Checks and argument templates of the quantise + GEMM pair for one key.
-    Inputs the fast path does not take (non-contiguous x, a host tensor, an
-    empty batch, operands that need converting) run the general path, which
-    checks them per call."""
+    """Checks and argument templates of the quantise + GEMM pair for one input
+    geometry.  Inputs the fast path does not take (non-contiguous x, a host
+    tensor, an empty batch, operands that need converting) run the general
+    path, which checks them per call."""
     c = _LinearCall()
     c.index = x.device.index
+    c.refs = (weakref.ref(weight), weakref.ref(wscale), None if bias is None else weakref.ref(bias))
+    c.versions = (weight._version, wscale._version, None if bias is None else bias._version)
     K = x.shape[-1]
     M = x.numel() // K if K > 0 else 0
     c.xq_shape = (M, K)
@@ -253,7 +301,6 @@ def _prepare_linear(x, weight, wscale, bias, out_features) -> _LinearCall:
         and wscale.is_cuda and wscale.device == x.device and wscale.dtype == torch.float32 and wscale.numel() == 1
         and (bias is None or (bias.is_cuda and bias.device == x.device and bias.dtype == torch.bfloat16
                               and bias.is_contiguous() and bias.numel() == out_features)))
-    c.keep = (weight, wscale, bias)
     if not c.fast:
         return c
     lib = _lib.load()
@@ -269,8 +316,6 @@ def _prepare_linear(x, weight, wscale, bias, out_features) -> _LinearCall:
     need = ctypes.c_int64(0)
     _lib.check(lib.qik_fp8_gemm_workspace_size(ctypes.byref(c.gargs), ctypes.byref(need)), "qik_fp8_gemm")
     c.gws_bytes = need.value
-    c.quantize = lib.qik_fp8_quantize
-    c.gemm = lib.qik_fp8_gemm_ws
     return c
 
 
@@ -297,13 +342,12 @@ class FP8Linear(nn.Module):
             out = torch.nn.functional.linear(x, w.to(x.dtype), self.bias)
             return out.to(x.dtype)
         weight, wscale, bias = self.weight, self.weight_scale, self.bias
-        key = (x.shape, x.stride(), x.dtype, x.device, weight.data_ptr(), weight._version, wscale.data_ptr(),
-               wscale._version, None if bias is None else (bias.data_ptr(), bias._version))
+        key = (x.shape, x.stride(), x.dtype, x.device)
         calls = self.__dict__.get("_calls")
         if calls is None:
             calls = self.__dict__["_calls"] = {}
         ent = calls.get(key)
-        if ent is None:
+        if ent is None or not ent.matches(weight, wscale, bias):
             ent = _prepare_linear(x, weight, wscale, bias, self.out_features)
             if len(calls) >= 8:
                 calls.clear()
@@ -311,10 +355,11 @@ class FP8Linear(nn.Module):
         idx = ent.index
         if ent.fast and x.data_ptr() % 16 == 0 and idx == torch.cuda.current_device():
             # quantise x and multiply: the argument structs of both launches
-            # are prepared per key, only the data pointers change per call
+            # are prepared per input geometry, only the data pointers change
+            lib = _lib.load()
             stream = torch._C._cuda_getCurrentRawStream(idx)
             ws = _QUANT_WS.get((idx, stream))
-            if ws is None or ws.numel() * 4 < ent.ws_bytes:
+            if ws is None or ws.numel() * 4 < ent.ws_bytes or torch.cuda.is_current_stream_capturing():
                 ws = _quant_workspace(x.device, stream, ent.ws_bytes)
             xq = torch.empty(ent.xq_shape, dtype=torch.float8_e4m3fn, device=x.device)
             s_a = torch.empty(1, dtype=torch.float32, device=x.device)
@@ -323,19 +368,33 @@ class FP8Linear(nn.Module):
             qa.x = x.data_ptr()
             qa.out = xq.data_ptr()
             qa.scale = s_a.data_ptr()
-            _lib.check(ent.quantize(ctypes.byref(qa), ws.data_ptr(), ws.numel() * 4, stream), "qik_fp8_quantize")
+            _lib.check(lib.qik_fp8_quantize(ctypes.byref(qa), ws.data_ptr(), ws.numel() * 4, stream),
+                       "qik_fp8_quantize")
             ga = _lib.QikFp8GemmArgs.from_buffer_copy(ent.gargs)
             ga.a = xq.data_ptr()
             ga.scale_a = s_a.data_ptr()
             ga.out = out.data_ptr()
             gws = _gemm_workspace(x.device, stream, ent.gws_bytes)
-            _lib.check(ent.gemm(ctypes.byref(ga), gws or None, ent.gws_bytes, stream), "qik_fp8_gemm")
+            _lib.check(lib.qik_fp8_gemm_ws(ctypes.byref(ga), None if gws is None else gws.data_ptr(), ent.gws_bytes,
+                                           stream), "qik_fp8_gemm")
         else:
             x2 = x.reshape(-1, x.shape[-1])
             xq, s_a = quantize_tensorwise(x2)
             out = fp8_linear(xq, weight, s_a, wscale, bias, torch.bfloat16)
         out = out.view(ent.result_shape)
         return out.to(x.dtype) if out.dtype != x.dtype else out
+
+    def _apply(self, fn, recurse=True):
+        # .to() / .cuda() / .half() replace the buffers: drop the launch cache
+        self.__dict__.pop("_calls", None)
+        return super()._apply(fn, recurse)
+
+    def __getstate__(self):
+        # copies and pickles carry the buffers, not the launch cache (ctypes
+        # structs of device addresses)
+        state = super().__getstate__()
+        state.pop("_calls", None)
+        return state
 
     @staticmethod
     def from_linear(linear: nn.Linear) -> "FP8Linear":

@@ -191,9 +191,11 @@ class ContiguousKVCache:
         device: torch.device | str = "cuda",
         dtype: torch.dtype = torch.bfloat16,
     ):
-        if dtype not in (torch.bfloat16, torch.float16):
-            # the store and attention kernels read 2-byte K/V elements
-            raise ValueError(f"slab dtype must be bfloat16 or float16, got {dtype}")
+        if torch.device(device).type != "cpu" and dtype not in (torch.bfloat16, torch.float16):
+            # the device store and the attention kernel read 2-byte K/V
+            # elements; a CPU slab (stored by torch's ops, as the reference's
+            # cache does) takes any dtype
+            raise ValueError(f"a device slab's dtype must be bfloat16 or float16, got {dtype}")
         self.v_fp8 = v_fp8
         self.num_layers = num_layers
         self.capacity = prefix_max

@@ -416,7 +416,7 @@ def test_fp8_quant_workspace_size_and_checks():
 
 def test_fp8_dequant_rejects_before_any_launch():
     lib = _lib.load()
-    assert lib.qik_fp8_dequant(0x10000, 0x20000, 0x30000, 64, _lib.DTYPE_FP32, None) == -3
+    assert lib.qik_fp8_dequant(0x10000, 0x20000, 0x30000, 64, 3, None) == -3       # fp32 is an output type now
     assert lib.qik_fp8_dequant(0x10000, 0x20000, 0x30000, -1, _lib.DTYPE_BF16, None) == -5
     assert lib.qik_fp8_dequant(0x10000, 0x20000, 0x30000, 0, _lib.DTYPE_BF16, None) == 0   # no work
     assert lib.qik_fp8_dequant(None, 0x20000, 0x30000, 64, _lib.DTYPE_BF16, None) == -1
@@ -426,8 +426,9 @@ def test_fp8_dequant_rejects_before_any_launch():
 
 def test_slab_store_fp8_takes_fp16_and_cache_rejects_other_dtypes():
     """An fp8 slab store validates for an fp16 source as for bf16 (the
-    reference quantises any dtype, kv_cache.py:36-42); the cache refuses
-    element types its kernels cannot read (4-byte fp32, 1-byte) up front."""
+    reference quantises any dtype, kv_cache.py:36-42); a device cache refuses
+    element types its kernels cannot read (4-byte fp32, 1-byte) up front,
+    before it allocates anything."""
     import torch
     import qwen_image_kernel_amd as qik
     lib = _lib.load()
@@ -437,7 +438,33 @@ def test_slab_store_fp8_takes_fp16_and_cache_rejects_other_dtypes():
         assert n.value == 2 * 64 * 4                  # B*H heads x 64 chunk scales
     for dt in (torch.float32, torch.float8_e4m3fn, torch.int16):
         with pytest.raises(ValueError, match="bfloat16 or float16"):
-            qik.ContiguousKVCache(1, 1, 16, 2, 128, device="cpu", dtype=dt)
+            qik.ContiguousKVCache(1, 1, 16, 2, 128, device="cuda", dtype=dt)
+
+
+@pytest.mark.parametrize("v_fp8", [False, True])
+def test_cpu_slab_takes_any_float_dtype_like_the_reference(v_fp8):
+    """A CPU slab is stored by the reference's torch ops (kv_cache.py:30-45),
+    so an fp32 CPU cache works as the reference's does: K copied, V copied or
+    quantised per (b, h) with scale max(amax/448, 1e-12)."""
+    import torch
+    import qwen_image_kernel_amd as qik
+    g = torch.Generator().manual_seed(5)
+    B, P, H, D = 2, 24, 3, 64
+    k = torch.randn(B, P, H, D, generator=g)
+    v = torch.randn(B, P, H, D, generator=g) * 3
+    cache = qik.ContiguousKVCache(2, B, P + 8, H, D, v_fp8=v_fp8, device="cpu", dtype=torch.float32)
+    cache.get_layer(1).store(k, v)
+    kk, vv = cache.get_layer(1).get()
+    assert kk.dtype == torch.float32 and torch.equal(kk, k)
+    assert int(cache.lengths[1]) == P
+    if v_fp8:
+        vt = v.transpose(1, 2)
+        scale = (vt.abs().amax(dim=(2, 3)) / 448.0).clamp_min(1e-12)
+        codes = (vt / scale[:, :, None, None]).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+        assert torch.equal(cache.v_scale[1], scale)
+        assert torch.equal(vv.transpose(1, 2).view(torch.uint8), codes.view(torch.uint8))
+    else:
+        assert torch.equal(vv, v)
 
 
 def test_kernel_layout_rule():

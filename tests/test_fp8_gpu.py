@@ -147,6 +147,13 @@ def test_dequant_bit_exact(qik):
     got = _dequant_weight(odd, s, torch.bfloat16)
     want = (odd.to(torch.bfloat16).float() * s).to(torch.bfloat16)
     assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    # fp32 (and wider) activations take the exact fp32 product (fp8.py:81-82)
+    for n in (64000, 1003):
+        ww = w.reshape(-1)[:n]
+        got = _dequant_weight(ww, s, torch.float32)
+        want = ww.to(torch.bfloat16).float() * s
+        assert got.dtype == torch.float32 and torch.equal(got.view(torch.int32), want.view(torch.int32))
+    assert _dequant_weight(w, s, torch.float64).dtype == torch.float32
 
 
 def _gemm_operands(M, N, K, seed, lda=None):
@@ -331,18 +338,59 @@ def test_fp8linear_forward_paths(qik):
     w = (fs.weight.to(torch.bfloat16).float() * fs.weight_scale).to(torch.bfloat16)
     want = torch.nn.functional.linear(x, w, fs.bias)
     assert torch.equal(fs(x), want)
+    # the same with fp32 activations: the weight is the fp32 product, unrounded
+    fs32 = qik.FP8Linear.from_linear(torch.nn.Linear(64, 512, bias=False, device=DEV))
+    x32 = torch.randn(3, 64, device=DEV)
+    w32 = fs32.weight.to(torch.bfloat16).float() * fs32.weight_scale
+    assert torch.equal(fs32(x32), torch.nn.functional.linear(x32, w32, None))
 
 
-def test_from_linear_cpu_weights_match_gpu(qik):
+def test_from_linear_cpu_and_device_weights_follow_torch_there(qik):
+    """A CPU weight is quantised on the CPU (torch's CPU ops: true divisions),
+    a device weight on the device (torch's device ops: the amax times the
+    reciprocal of 448), each bit-identical to the reference's ops where the
+    weight lives; the two agree except where the scales differ in the last bit."""
     torch.manual_seed(2)
     lin = torch.nn.Linear(1024, 512, bias=True, dtype=torch.bfloat16)
     fc = qik.FP8Linear.from_linear(lin)
     assert fc.weight.device.type == "cpu"
+    s_cpu = (lin.weight.data.float().abs().amax() / 448.0).clamp_min(1e-12)
+    w_cpu = (lin.weight.data.float() / s_cpu).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+    assert torch.equal(fc.weight.view(torch.uint8), w_cpu.view(torch.uint8))
     fg = qik.FP8Linear.from_linear(lin.to(DEV))
-    assert torch.equal(fc.weight.view(torch.uint8), fg.weight.view(torch.uint8).cpu())
-    assert torch.equal(fc.weight_scale, fg.weight_scale.cpu())
-    wq, s = of.quantize_weight_tensorwise(lin.weight.detach().float().cpu().numpy())
-    np.testing.assert_array_equal(fc.weight.view(torch.uint8).numpy(), wq)
+    wq, sw = torch_weight_quant(lin.weight.data.float())
+    assert torch.equal(fg.weight.view(torch.uint8), wq.view(torch.uint8)) and torch.equal(fg.weight_scale, sw)
+    if torch.equal(fc.weight_scale, fg.weight_scale.cpu()):
+        assert torch.equal(fc.weight.view(torch.uint8), fg.weight.view(torch.uint8).cpu())
+
+
+def test_fp8linear_module_contract_after_a_forward(qik):
+    """After a forward the module deep-copies and pickles, and .to('cpu')
+    releases its device weight (the reference's runtime moves the DiT off the
+    GPU before the VAE decode, runtime.py:643-645)."""
+    import copy
+    import gc
+    import pickle
+    torch.manual_seed(3)
+    N, K = 4096, 3072
+    fq = qik.FP8Linear.from_linear(torch.nn.Linear(K, N, bias=True, dtype=torch.bfloat16, device=DEV))
+    x = torch.randn(256, K, device=DEV, dtype=torch.bfloat16)
+    want = fq(x)
+    assert "_calls" in fq.__dict__
+    c = copy.deepcopy(fq)
+    assert torch.equal(c(x), want)
+    pickle.dumps(fq)
+    del c
+    gc.collect()
+    torch.cuda.synchronize()
+    before = torch.cuda.memory_allocated(DEV)
+    fq.to("cpu")
+    gc.collect()
+    after = torch.cuda.memory_allocated(DEV)
+    assert before - after >= N * K, (before, after)
+    assert fq.weight.device.type == "cpu"
+    fq.to(DEV)
+    assert torch.equal(fq(x), want)
 
 
 def test_convert_linears_fp8_and_state_dict(qik):

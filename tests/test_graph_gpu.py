@@ -74,3 +74,37 @@ def test_layer_steps_under_graph_replay():
         eager = _layer(x)  # eager steps on the default stream between replays
         torch.cuda.synchronize()
         assert torch.equal(eager[0], want[0]), f"eager after replay {i}"
+
+
+def test_fp8_linear_under_graph_replay():
+    """FP8Linear (quantiser + GEMM, and the K-split GEMM with its workspace)
+    captured in a graph: every replay equals the eager result, with eager
+    calls of the same module between replays."""
+    print("case fp8 linear graph", flush=True)
+    torch.manual_seed(7)
+    mods = [qik.FP8Linear.from_linear(torch.nn.Linear(K, N, bias=True, dtype=torch.bfloat16, device=DEV))
+            for K, N in ((3072, 3072), (12288, 3072))]
+    xs = [torch.randn(256, m.in_features, device=DEV, dtype=torch.bfloat16) for m in mods]
+    want = [m(x).clone() for m, x in zip(mods, xs)]
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for m, x in zip(mods, xs):
+            m(x)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        got = [m(x) for m, x in zip(mods, xs)]
+    for i in range(4):
+        for t in got:
+            t.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        for j, (a, b) in enumerate(zip(got, want)):
+            assert torch.equal(a, b), f"replay {i}: linear {j}"
+        eager = [m(x) for m, x in zip(mods, xs)]
+        torch.cuda.synchronize()
+        for a, b in zip(eager, want):
+            assert torch.equal(a, b), f"eager after replay {i}"

@@ -131,6 +131,29 @@ def test_cpu_baseline_sdpa_matches_oracle():
                                atol=2e-6, rtol=0)
 
 
+@pytest.mark.parametrize("with_slab", [False, True])
+def test_timed_cpu_baseline_equals_the_explicit_mask_sdpa(with_slab):
+    """CpuSdpaBaseline (the class the benchmark times as its CPU baseline)
+    computes, per (b, h), what sdpa_explicit_mask_cpu does, and both are the
+    fp32 oracle: the timed work is the reference's CPU path, not less."""
+    segs, S = ol.make_segments([("text", 20), ("img", 44), ("img", 36)])
+    B, H, D = 2, 3, 64
+    q, k, v = _qkv(B, S, H, D, 14)
+    P = 0
+    ck = cv = sc = None
+    if with_slab:
+        P = 40
+        ck, cv, sc = _fp8_slab(B, P, H, D, 15)
+    L = ol.build_prefix_lengths(segs, S, S) + P
+    base = oa.CpuSdpaBaseline(q, k, v, L, ck, cv, sc)
+    want = oa.sdpa_explicit_mask_cpu(q, k, v, L, None, ck, cv, sc)
+    assert base.pairs == int(sum(int(x) + 1 for x in L))
+    for b in range(B):
+        for h in range(H):
+            assert torch.equal(base.run(b, h), want[b, :, h])
+    np.testing.assert_allclose(want.numpy(), oa.attention_fp32(q, k, v, L, None, ck, cv, sc), atol=2e-6, rtol=0)
+
+
 @pytest.mark.parametrize("bad", ["drop_scale", "swap_qk_sign"])
 def test_planted_mistakes_are_caught(bad):
     """A plausible oracle mistake must fail the fp64 comparison used above."""
