@@ -917,7 +917,10 @@ __global__ void __launch_bounds__(NTHREADS * KSPLIT, KSPLIT == 1 ? 2 : 1) attn_f
     }
     const float l_tot = pair_sum(l_part);
     // a NaN row sum (non-finite inputs, or a timed-out group barrier) gives NaN rows
-    const float inv = (l_tot > 0.0f) ? 1.0f / l_tot : (l_tot == l_tot ? 0.0f : l_tot);
+    // (written as selects around one division, so that no branch is formed:
+    // 1/l for l > 0, 1 * (l - l) otherwise, which is 0 for l = 0 and NaN for NaN)
+    const bool pos = l_tot > 0.0f;
+    const float inv = (1.0f / (pos ? l_tot : 1.0f)) * (pos ? 1.0f : l_tot - l_tot);
     if (pulled && tid == 0) snext = gx + (int)pend;
     if constexpr (V_FP8 || KV) {
       // kernels that write LDS inside the tile loop (the fp8 V dequantisation,
