@@ -479,7 +479,7 @@ def fp8_linear_ops(qik, dev, with_cpu: bool) -> dict:
         qa = f8.quant_args(x.reshape(-1), xq, sa, _lib.FP8_ACTIVATION)
         nws = ctypes.c_int64()
         _lib.check(lib.qik_fp8_quant_workspace_size(ctypes.byref(qa), ctypes.byref(nws)), "workspace size")
-        qws = torch.empty(max(nws.value, 4), dtype=torch.uint8, device=dev)
+        qws = torch.zeros(max(nws.value, 4), dtype=torch.uint8, device=dev)  # zero before first use
         q_us = _batch_us(lambda: lib.qik_fp8_quantize(ctypes.byref(qa), qws.data_ptr(), nws.value, stream), 30)
         api_us, host_us = _batch_us(lambda: fq(x), 30), _host_us(lambda: fq(x), 100)
         flops = 2.0 * M * N * K

@@ -66,10 +66,18 @@ typedef struct qik_fp8_quant_args {
   int64_t n;                  /* elements, 1 <= n < 2^40                             */
 } qik_fp8_quant_args;
 
-/* Two launches: per-block partial maxima into the caller's workspace (at least
- * qik_fp8_quant_workspace_size bytes, 4-byte aligned, contents irrelevant: every
- * launch writes what it reads), then the codes.  QIK_ERR_WORKSPACE for a
- * missing, misaligned or short workspace. */
+/* One launch when x fits the registers of the workgroups the device holds at
+ * once (about 109 MB of bf16/fp16 on MI355X, half that of fp32): every
+ * workgroup reads its share of x once, the workgroups exchange their maxima
+ * through the workspace, and each writes its codes.  Larger inputs take two
+ * launches: per-block partial maxima into the workspace, then the codes (x
+ * read twice).  The workspace (at least qik_fp8_quant_workspace_size bytes,
+ * 4-byte aligned) must be zero-filled before its first use; every call leaves
+ * it fit for the next call on the same stream (calls that overlap must not
+ * share one).  QIK_ERR_WORKSPACE for a missing, misaligned or short
+ * workspace.  If a workgroup of a one-pass launch cannot start within tens of
+ * milliseconds (the device fully occupied by other work for that long), the
+ * launch writes a NaN scale and NaN codes rather than wait without bound. */
 int qik_fp8_quant_workspace_size(const qik_fp8_quant_args* args, int64_t* bytes);
 int qik_fp8_quantize(const qik_fp8_quant_args* args, void* workspace, int64_t workspace_bytes, void* stream);
 

@@ -29,6 +29,7 @@
 #include <algorithm>
 #include <cmath>
 #include <thread>
+#include <utility>
 #include <vector>
 
 #include "qik_fp8.h"
@@ -69,14 +70,25 @@ constexpr int QT = 256;          // threads per block
 constexpr int QU = 4;            // 16-byte vectors per thread in flight
 constexpr int MAX_PARTS = 1024;  // blocks of the maximum pass = workspace words
 
+// Workspace of the quantiser (32-bit words): QCTL words of control (word 0:
+// the generation of the next one-pass launch), RES_SLOTS 64-bit slots (the
+// maximum each workgroup of a one-pass launch publishes, tagged with the
+// launch's generation + 1), then MAX_PARTS partial maxima of the two-pass
+// form.  Zero-filled once; no launch needs it cleared again.
+constexpr int QCTL = 64;
+constexpr int RES_SLOTS = 1024;  // most workgroups of a one-pass launch
+constexpr int QWS_WORDS = QCTL + 2 * RES_SLOTS + MAX_PARTS;
+
 struct QuantParams {
   const char* x;
   unsigned char* out;
   float* scale;
   unsigned* part;  // [nparts] max |x| of each block's share, as fp32 bit patterns
+  unsigned* ctl;   // one-pass launch: control words and slots (zero between launches)
   int64_t n;       // elements
   int64_t nvec;    // whole 16-byte vectors of x
   int nparts;
+  int spin;        // one-pass launch: polls of a slot before the launch gives up (scale NaN)
 };
 
 template <int DT>
@@ -254,6 +266,129 @@ __global__ void __launch_bounds__(QT) cast_kernel(const QuantParams p) {
     }
   }
   if (blockIdx.x == gridDim.x - 1) {
+    for (int64_t i = p.nvec * PV + threadIdx.x; i < p.n; i += QT)
+      p.out[i] = (unsigned char)cvt2(quant_value<MODE>(E::get(p.x, i), scale, inv, ex), 0.0f);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// One-pass quantiser
+// ---------------------------------------------------------------------------
+//
+// x is read from HBM once.  Every workgroup of the launch is resident at once
+// (the host sizes the grid to the device's occupancy) and keeps its share of x
+// in registers, VPT 16-byte vectors per thread.  Each workgroup publishes its
+// maximum in a 64-bit slot of its own, tagged with the launch's generation + 1
+// (written through to device scope), then reads every slot until all carry
+// that tag: no workgroup waits on a shared counter and no atomic is needed.
+// Each then forms the scale and writes its codes from the registers.
+// Workgroup 0, once it has seen every slot (so every workgroup has read the
+// generation), advances the generation for the next launch; stale slots of
+// earlier launches carry other tags, so nothing is ever cleared.  A slot that
+// stays untagged for `spin` polls (a workgroup that never became resident)
+// makes the launch write a NaN scale and NaN codes, never plausible numbers.
+
+__device__ __forceinline__ void store_dev(unsigned* p, unsigned v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned load_dev(unsigned* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_dev64(uint64_t* p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t load_dev64(uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int DT, int MODE, int VPT>
+__global__ void __launch_bounds__(QT, 2) quant_onepass_kernel(const QuantParams p) {
+#pragma clang fp contract(off)
+  using E = Elem<DT>;
+  constexpr int PV = E::PER_VEC;
+  // buffer accesses: one 32-bit lane offset plus a constant per vector, and
+  // vectors past the end read as zero / are not written (x of a one-pass
+  // launch is far below 4 GiB)
+  const uint32_t v0 = blockIdx.x * (uint32_t)(QT * VPT) + threadIdx.x;
+  const __amdgpu_buffer_rsrc_t xs = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(p.x), (short)0,
+                                                                      (int)(p.nvec * 16), 0x00020000);
+  const __amdgpu_buffer_rsrc_t os = __builtin_amdgcn_make_buffer_rsrc(p.out, (short)0, (int)(p.nvec * PV),
+                                                                      0x00020000);
+  u32x4 raw[VPT];
+#pragma unroll
+  for (int u = 0; u < VPT; ++u)
+    raw[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xs, v0 * 16u, u * QT * 16, 0));
+  unsigned m = 0;
+#pragma unroll
+  for (int u = 0; u < VPT; ++u) {
+    float f[PV];
+    E::unpack(raw[u], f);
+#pragma unroll
+    for (int i = 0; i < PV; ++i) m = max(m, abs_bits(f[i]));
+  }
+  // hold x packed across the exchange: without the empty asm the compiler
+  // keeps the unpacked fp32 values of the maximum pass for the codes, twice
+  // the registers
+#pragma unroll
+  for (int u = 0; u < VPT; ++u) asm volatile("" : "+v"(raw[u]));
+  const bool last_wg = blockIdx.x == gridDim.x - 1;
+  if (last_wg) {
+    for (int64_t i = p.nvec * PV + threadIdx.x; i < p.n; i += QT) m = max(m, abs_bits(E::get(p.x, i)));
+  }
+  __shared__ unsigned sh_gen;
+  if (threadIdx.x == 0) sh_gen = load_dev(p.ctl);
+  m = block_max(m);  // its barrier also publishes sh_gen
+  const uint64_t tag = (uint64_t)(sh_gen + 1u) << 32;
+  uint64_t* const slots = reinterpret_cast<uint64_t*>(p.ctl + QCTL);
+  if (threadIdx.x == 0) store_dev64(slots + blockIdx.x, tag | m);
+  __syncthreads();  // thread 0 has read block_max's words before they are reused
+
+  unsigned mm = 0;
+  int missing = 0;
+  for (int s = threadIdx.x; s < (int)gridDim.x; s += QT) {
+    uint64_t w = load_dev64(slots + s);
+    for (int i = 0; i < p.spin && (w & 0xffffffff00000000ull) != tag; ++i) {
+      __builtin_amdgcn_s_sleep(1);
+      w = load_dev64(slots + s);
+    }
+    missing |= (w & 0xffffffff00000000ull) == tag ? 0 : 1;
+    mm = max(mm, (unsigned)w);
+  }
+  const int bad = __syncthreads_or(missing);
+  mm = block_max(mm);
+  __shared__ float sh_scale;
+  if (threadIdx.x == 0) {
+    const float sc = bad ? __builtin_nanf("") : scale_of(mm);
+    sh_scale = sc;
+    if (blockIdx.x == 0) {
+      p.scale[0] = sc;
+      // every workgroup has published, hence read the generation
+      store_dev(p.ctl, sh_gen + 1u);
+    }
+  }
+  __syncthreads();
+  const float scale = sh_scale;
+  const float inv = 1.0f / scale;  // IEEE division (the reference's cast kernel: 1.0 / scale)
+  const bool ex = __builtin_isfinite(scale);
+#pragma unroll
+  for (int u = 0; u < VPT; ++u) {
+    float f[PV];
+    E::unpack(raw[u], f);
+    if constexpr (PV == 8) {
+      u32x2 o;
+      o.x = cvt2(quant_value<MODE>(f[0], scale, inv, ex), quant_value<MODE>(f[1], scale, inv, ex)) |
+            (cvt2(quant_value<MODE>(f[2], scale, inv, ex), quant_value<MODE>(f[3], scale, inv, ex)) << 16);
+      o.y = cvt2(quant_value<MODE>(f[4], scale, inv, ex), quant_value<MODE>(f[5], scale, inv, ex)) |
+            (cvt2(quant_value<MODE>(f[6], scale, inv, ex), quant_value<MODE>(f[7], scale, inv, ex)) << 16);
+      __builtin_amdgcn_raw_buffer_store_b64(o, os, v0 * 8u, u * QT * 8, 0);
+    } else {
+      __builtin_amdgcn_raw_buffer_store_b32(
+          cvt2(quant_value<MODE>(f[0], scale, inv, ex), quant_value<MODE>(f[1], scale, inv, ex)) |
+              (cvt2(quant_value<MODE>(f[2], scale, inv, ex), quant_value<MODE>(f[3], scale, inv, ex)) << 16),
+          os, v0 * 4u, u * QT * 4, 0);
+    }
+  }
+  if (last_wg) {
     for (int64_t i = p.nvec * PV + threadIdx.x; i < p.n; i += QT)
       p.out[i] = (unsigned char)cvt2(quant_value<MODE>(E::get(p.x, i), scale, inv, ex), 0.0f);
   }
@@ -762,19 +897,94 @@ int quant_parts(const qik_fp8_quant_args* a) {
   return (int)std::max<int64_t>(1, std::min<int64_t>(parts, MAX_PARTS));
 }
 
+// Vectors per thread of the one-pass launches, smallest first: dense enough
+// that most inputs find a size whose grid nearly fills the CUs with one
+// workgroup each (measured at [4352, 3072] bf16 on MI355X: 252 workgroups of
+// 26 vectors 10.7 us, 204 of 32 12.0 us, 272 of 24 13.2 us).
+constexpr int ONEPASS_N = 10;
+constexpr int ONEPASS_VPT[ONEPASS_N] = {4, 8, 12, 16, 20, 24, 26, 32, 40, 52};
+constexpr int ONEPASS_DEFAULT_SPIN = 1 << 16;  // polls of one device-scope round trip each: tens of ms
+
+template <int DT, int MODE, int VPT>
+const void* onepass_fn() {
+  return (const void*)quant_onepass_kernel<DT, MODE, VPT>;
+}
+
+// Workgroups of one one-pass variant that the current device holds at once
+// (occupancy x CUs, at most RES_SLOTS), cached per device; 0 if unknown.
+int onepass_capacity(const void* fn, int which) {
+  static int cache[64][3 * 2 * ONEPASS_N];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  int c = __atomic_load_n(&cache[dev][which], __ATOMIC_RELAXED);
+  if (c > 0) return c;
+  const int cus = device_cus();
+  int occ = 0;
+  if (cus <= 0 || hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, QT, 0) != hipSuccess || occ <= 0) return 0;
+  c = std::min(occ * cus, RES_SLOTS);
+  __atomic_store_n(&cache[dev][which], c, __ATOMIC_RELAXED);
+  return c;
+}
+
+template <int DT, int MODE, int... I>
+const void* onepass_pick_seq(int i, std::integer_sequence<int, I...>) {
+  const void* fns[] = {onepass_fn<DT, MODE, ONEPASS_VPT[I]>()...};
+  return fns[i];
+}
+template <int DT, int MODE>
+const void* onepass_pick(int i) {
+  return onepass_pick_seq<DT, MODE>(i, std::make_integer_sequence<int, ONEPASS_N>{});
+}
+
+// The one-pass launch for n elements: kernel and grid, or fn = NULL when x
+// does not fit the registers of the resident workgroups (the two-pass form).
+struct OnePass {
+  const void* fn;
+  int64_t grid;
+};
+
+// The fewest workgroups win: every workgroup reads every slot, so the exchange
+// grows with the square of the grid.  The smallest VPT that needs at most one
+// workgroup per CU, else the smallest that fits the resident workgroups.
 template <int DT>
-int launch_quant(const qik_fp8_quant_args* a, unsigned* part, hipStream_t s) {
+OnePass plan_onepass(const qik_fp8_quant_args* a) {
+  constexpr int PV = Elem<DT>::PER_VEC;
+  const int64_t nvec = std::max<int64_t>(1, a->n / PV);
+  if (nvec * 16 >= (int64_t)INT_MAX) return OnePass{nullptr, 0};  // 32-bit buffer offsets
+  const int cus = device_cus();
+  OnePass fit{nullptr, 0};
+  for (int i = 0; i < ONEPASS_N; ++i) {
+    const int64_t grid = (nvec + (int64_t)QT * ONEPASS_VPT[i] - 1) / ((int64_t)QT * ONEPASS_VPT[i]);
+    const void* fn = a->mode == QIK_FP8_ACTIVATION ? onepass_pick<DT, QIK_FP8_ACTIVATION>(i)
+                                                   : onepass_pick<DT, QIK_FP8_WEIGHT>(i);
+    const int dt_i = DT == QIK_DTYPE_BF16 ? 0 : DT == QIK_DTYPE_FP16 ? 1 : 2;
+    const int cap = onepass_capacity(fn, (dt_i * 2 + a->mode) * ONEPASS_N + i);
+    if (cap <= 0 || grid > cap) continue;
+    if (grid <= cus) return OnePass{fn, grid};
+    if (fit.fn == nullptr) fit = OnePass{fn, grid};
+  }
+  return fit;
+}
+
+template <int DT>
+int launch_quant(const qik_fp8_quant_args* a, unsigned* ws, hipStream_t s) {
   constexpr int PV = Elem<DT>::PER_VEC;
   QuantParams p;
   memset(&p, 0, sizeof(p));
   p.x = static_cast<const char*>(a->x);
   p.out = static_cast<unsigned char*>(a->out);
   p.scale = a->scale;
-  p.part = part;
+  p.ctl = ws;
+  p.part = ws + QCTL + 2 * RES_SLOTS;
   p.n = a->n;
   p.nvec = a->n / PV;
   p.nparts = quant_parts(a);
+  p.spin = ONEPASS_DEFAULT_SPIN;
   void* args[] = {&p};
+  const OnePass op = plan_onepass<DT>(a);
+  if (op.fn != nullptr)
+    return hipLaunchKernel(op.fn, dim3((unsigned)op.grid), dim3(QT), args, 0, s) == hipSuccess ? QIK_OK
+                                                                                                 : QIK_ERR_LAUNCH;
   if (hipLaunchKernel((const void*)amax_kernel<DT>, dim3((unsigned)p.nparts), dim3(QT), args, 0, s) != hipSuccess)
     return QIK_ERR_LAUNCH;
   const int64_t grid = std::max<int64_t>(1, (p.nvec + QT * QU - 1) / (QT * QU));
@@ -1065,7 +1275,7 @@ int qik_fp8_quant_workspace_size(const qik_fp8_quant_args* a, int64_t* bytes) {
   *bytes = 0;
   const int st = qik_fp8::validate_quant(a);
   if (st != QIK_OK) return st;
-  *bytes = (int64_t)qik_fp8::quant_parts(a) * (int64_t)sizeof(unsigned);
+  *bytes = (int64_t)qik_fp8::QWS_WORDS * (int64_t)sizeof(unsigned);
   return QIK_OK;
 }
 
@@ -1073,7 +1283,7 @@ int qik_fp8_quantize(const qik_fp8_quant_args* a, void* workspace, int64_t works
   using namespace qik_fp8;
   const int st = validate_quant(a);
   if (st != QIK_OK) return st;
-  const int64_t need = (int64_t)quant_parts(a) * (int64_t)sizeof(unsigned);
+  const int64_t need = (int64_t)QWS_WORDS * (int64_t)sizeof(unsigned);
   if (workspace == nullptr || workspace_bytes < need || !aligned_to(workspace, 4)) return QIK_ERR_WORKSPACE;
   unsigned* part = static_cast<unsigned*>(workspace);
   const hipStream_t s = static_cast<hipStream_t>(stream);

@@ -59,8 +59,8 @@ _OUT_DTYPES = {torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_FP16}
 # element types qik_fp8_dequant writes
 _DEQUANT_DTYPES = _IN_DTYPES
 
-# partial-maximum workspace of the quantiser, one per (device, stream); the
-# kernels write every word they read, so it is never cleared
+# workspace of the quantiser, one per (device, stream): zero-filled once when
+# created, and every call leaves it that way (include/qik_fp8.h)
 _QUANT_WS: dict = {}
 _GEMM_WS: dict = {}   # (device index, stream) -> fp32 workspace of the K-split GEMMs
 
@@ -74,13 +74,14 @@ def _quant_workspace(dev: torch.device, stream: int, nbytes: int) -> torch.Tenso
     capture a fresh one from the graph's pool, so that replays of different
     graphs (or a replay beside eager work) never share one."""
     if torch.cuda.is_current_stream_capturing():
-        return torch.empty(max(nbytes // 4, 1024), dtype=torch.int32, device=dev)
+        # torch.zeros records a fill kernel, not a memset node
+        return torch.zeros(max(nbytes // 4, 1024), dtype=torch.int32, device=dev)
     key = (dev.index, stream)
     ws = _QUANT_WS.get(key)
     if ws is None or ws.numel() * 4 < nbytes:
         if len(_QUANT_WS) >= 64:
             _QUANT_WS.clear()
-        ws = _QUANT_WS[key] = torch.empty(max(nbytes // 4, 1024), dtype=torch.int32, device=dev)
+        ws = _QUANT_WS[key] = torch.zeros(max(nbytes // 4, 1024), dtype=torch.int32, device=dev)
     return ws
 
 

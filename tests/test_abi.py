@@ -395,23 +395,20 @@ def _quant_args(**kw):
 def test_fp8_quant_workspace_size_and_checks():
     lib = _lib.load()
     n = ctypes.c_int64(-1)
-    assert lib.qik_fp8_quant_workspace_size(ctypes.byref(_quant_args()), ctypes.byref(n)) == 0
-    # one partial maximum per block of 256 threads x 8 vectors, at most 1024
-    assert n.value == 4 * min(1024, -(-(1536 * 4096 // 8) // 2048))
-    assert lib.qik_fp8_quant_workspace_size(ctypes.byref(_quant_args(n=3)), ctypes.byref(n)) == 0
-    assert n.value == 4
-    assert lib.qik_fp8_quant_workspace_size(ctypes.byref(_quant_args(n=1 << 36)), ctypes.byref(n)) == 0
-    assert n.value == 4 * 1024
+    # one size for every n: 64 control words, 1024 64-bit one-pass slots, 1024 two-pass partial maxima
+    for nn in (1536 * 4096, 3, 1 << 36):
+        assert lib.qik_fp8_quant_workspace_size(ctypes.byref(_quant_args(n=nn)), ctypes.byref(n)) == 0
+        assert n.value == 4 * (64 + 2 * 1024 + 1024)
     for kw, code in [({"n": 0}, -5), ({"dtype": 5}, -3), ({"mode": 2}, -3), ({"x": None}, -1),
                      ({"x": 0x10008}, -8), ({"out": 0x20004}, -8), ({"dtype": _lib.DTYPE_FP32, "out": 0x20004}, 0),
                      ({"reserved0": 1}, -2)]:
         assert lib.qik_fp8_quant_workspace_size(ctypes.byref(_quant_args(**kw)), ctypes.byref(n)) == code, kw
-    buf = (ctypes.c_uint32 * 1024)()
+    buf = (ctypes.c_uint32 * 4096)()
     base = ctypes.addressof(buf)
     WS = -12
-    assert lib.qik_fp8_quantize(ctypes.byref(_quant_args()), None, 4096, None) == WS
-    assert lib.qik_fp8_quantize(ctypes.byref(_quant_args()), base, 4, None) == WS
-    assert lib.qik_fp8_quantize(ctypes.byref(_quant_args()), base + 2, 4096, None) == WS
+    assert lib.qik_fp8_quantize(ctypes.byref(_quant_args()), None, 16384, None) == WS
+    assert lib.qik_fp8_quantize(ctypes.byref(_quant_args()), base, 12540, None) == WS
+    assert lib.qik_fp8_quantize(ctypes.byref(_quant_args()), base + 2, 16384, None) == WS
 
 
 def test_fp8_dequant_rejects_before_any_launch():

@@ -91,6 +91,27 @@ def test_quantiser_bit_exact_vs_torch_ops(qik, shape, dtype, kind, which):
         np.testing.assert_array_equal(codes(got_q), oq)
 
 
+def test_quantiser_one_pass_and_two_pass_forms_in_turn(qik):
+    """Inputs that fit the registers of the resident workgroups take the
+    one-pass launch (maxima exchanged through the workspace); larger ones the
+    two-pass form.  Alternating them on one stream's workspace checks that
+    every call leaves the workspace ready for the next; each call is
+    bit-identical to torch's ops.  The two-pass case (72M bf16 elements) is
+    past the one-pass capacity of an MI355X (512 workgroups x 256 threads x 52
+    vectors of 8)."""
+    print("case quantiser one-pass / two-pass alternation", flush=True)
+    shapes = [((4352, 3072), torch.bfloat16), ((9000, 8000), torch.bfloat16), ((4352, 12288), torch.bfloat16),
+              ((333, 257), torch.float32), ((9000, 8000), torch.bfloat16), ((1, 1), torch.bfloat16),
+              ((4352, 3072), torch.bfloat16)]
+    for i, (shape, dt) in enumerate(shapes):
+        x = _inputs(shape, dt, 70 + i, "wide" if i % 2 else "normal")
+        got_q, got_s = qik.quantize_tensorwise(x)
+        want_q, want_s = torch_act_quant(x)
+        assert torch.equal(got_s, want_s), (shape, got_s, want_s)
+        assert torch.equal(got_q.view(torch.uint8), want_q.view(torch.uint8)), shape
+        del x, got_q, want_q
+
+
 @pytest.mark.parametrize("amax", [1.0, 448.0, 3.0, 2.0 ** -20, 2.0 ** 20, 1e-30, 1e30, 1e-13, 5e-10, 7.0, 0.1,
                                   1000.0])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
