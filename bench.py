@@ -85,12 +85,49 @@ def copy_calibration(mb: int) -> None:
     print(json.dumps({"copy_calibration_bytes_per_copy": n * 4, "copies": 5}), flush=True)
 
 
-def all_workloads() -> None:
+def cpu_leg(wl, inp, out, budget_s: float) -> dict:
+    """The CPU baseline leg of one workload: torch explicit-mask SDPA in fp32
+    (the reference's CPU path) on the host cores, timed per (b, h) on a
+    bounded sample of heads of the layer the GPU just computed; and the GPU
+    output of those heads against it (max-abs and mean-abs over every element
+    of the sampled heads, the parity bar being 2e-2 / 2e-3)."""
+    import torch
+
+    from oracle import attention as oa
+
+    cpu = {k: (v.cpu() if isinstance(v, torch.Tensor) else v) for k, v in inp.items()}
+    bl = oa.CpuSdpaBaseline(cpu["query"], cpu["key"], cpu["value"], wl.lengths(), cpu["cache_k"], cpu["cache_v"],
+                            cpu["cache_v_scale"])
+    got = out.float().cpu()
+    heads, elapsed, max_abs, sum_abs, n = [], 0.0, 0.0, 0.0, 0
+    pairs = [(b, h) for h in range(wl.H) for b in range(wl.B)]
+    for b, h in pairs:
+        t0 = time.perf_counter()
+        ref = bl.run(b, h)
+        elapsed += time.perf_counter() - t0
+        d = (got[b, :, h] - ref).abs()
+        max_abs = max(max_abs, float(d.max()))
+        sum_abs += float(d.sum())
+        n += d.numel()
+        heads.append((b, h))
+        if elapsed >= budget_s:
+            break
+    flops = 4 * wl.D * bl.pairs * len(heads)
+    return {"cpu_tflops": round(flops / elapsed / 1e12, 6), "cpu_seconds": round(elapsed, 3),
+            "cpu_heads": len(heads), "cpu_threads": torch.get_num_threads(), "cpu_model": cpu_model(),
+            "cpu_what": "fp32 F.scaled_dot_product_attention with a bool [SQ, KV] mask per (b, h), fp8 V dequantised first",
+            "max_abs_vs_cpu": float(f"{max_abs:.3e}"), "mean_abs_vs_cpu": float(f"{sum_abs / n:.3e}"),
+            "heads_compared": len(heads)}
+
+
+def all_workloads(cpu_seconds: float = 3.0) -> None:
     """Kernel time of every workload of the benchmark set through qik_attn_fwd_ws.
 
     Per workload: 8 independent layers launched back to back (multiref_cfg:
     4), 3 warm-up passes, then 5 groups of 4 passes with HIP events around
-    each group; the median group gives the time per launch.
+    each group; the median group gives the time per launch.  Then the CPU
+    baseline leg (``cpu_leg``) on about ``cpu_seconds`` of heads of the first
+    layer, with the GPU output of those heads compared against it.
     """
     import ctypes
 
@@ -142,6 +179,9 @@ def all_workloads() -> None:
                      "pct_bf16_peak": round(100 * tf / PEAK_BF16_TFLOPS, 2), "layers": nl,
                      "shape": [wl.B, wl.SQ, wl.H, wl.D], "P": wl.P, "SN": wl.SN,
                      "unmasked_gflop": round(wl.flops() / 1e9, 3)}
+        if cpu_seconds > 0:
+            res[name].update(cpu_leg(wl, layers[0], calls[0][3], cpu_seconds))
+            res[name]["gpu_over_cpu"] = round(res[name]["tflops"] / res[name]["cpu_tflops"], 1)
         print(name, json.dumps(res[name]), file=sys.stderr, flush=True)
         if name in ("t2i_1024", "edit_768"):
             runs.append((name, run))
@@ -523,7 +563,7 @@ def main():
         copy_calibration(args.copy_calibration_mb)
         return
     if args.all_workloads:
-        all_workloads()
+        all_workloads(min(args.cpu_seconds, 4.0))
         return
 
     import torch
