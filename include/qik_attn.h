@@ -41,7 +41,7 @@ enum qik_status {
   QIK_ERR_NULL_ARG = -1,      /* a required pointer is NULL                          */
   QIK_ERR_ABI_VERSION = -2,   /* args->abi_version != QIK_ABI_VERSION                */
   QIK_ERR_DTYPE = -3,         /* q/k/v dtype not bf16/fp16 (triton_attention.py:190) */
-  QIK_ERR_HEAD_DIM = -4,      /* D not in {64, 128}                                  */
+  QIK_ERR_HEAD_DIM = -4,      /* D not in {32, 64, 128, 256}                         */
   QIK_ERR_SHAPE = -5,         /* negative or oversized B/SQ/SN/P/H, or a K/V row stride >= 2^31/64 bytes */
   QIK_ERR_CACHE = -6,         /* cache flag / P / pointers inconsistent (:192-196)   */
   QIK_ERR_FP8_SCALE = -7,     /* fp8 V without scale, without cache, or non-bf16 (:213-216, :159) */

@@ -40,7 +40,7 @@ typedef struct qik_rms_rope_args {
   const float* weight;        /* [D] fp32 RMSNorm weight                             */
   const float* cos;           /* [S, D/2] fp32, contiguous                           */
   const float* sin;           /* [S, D/2] fp32, contiguous                           */
-  int64_t B, S, H, D;         /* D in {64, 128}                                      */
+  int64_t B, S, H, D;         /* D in {32, 64, 128, 256}                             */
   int64_t stride_x[3];        /* b, s, h                                             */
   int64_t stride_out[3];      /* b, s, h                                             */
   float eps;
@@ -70,7 +70,7 @@ typedef struct qik_slab_store_args {
   void* k_dst;                /* slab K of the layer                                 */
   void* v_dst;                /* slab V of the layer                                 */
   float* v_scale;             /* [B*H] fp32 (v_fp8 only, else NULL)                  */
-  int64_t B, P, H, D;         /* D in {64, 128}                                      */
+  int64_t B, P, H, D;         /* D in {32, 64, 128, 256}                             */
   int64_t stride_k[3];        /* b, p, h of k                                        */
   int64_t stride_v[3];        /* b, p, h of v                                        */
   int64_t stride_k_dst[3];    /* b, h, p of k_dst                                    */

@@ -281,12 +281,15 @@ __device__ __forceinline__ int wave_reduce_i32(int x) {
 // instructions, so instruction r adds r * (1024/ROWB)*NWAVES rows to the offset
 // returned here (the one of r = 0).
 template <int D>
-__device__ __forceinline__ uint32_t dma_lane_offset(int lane, int wave, int row_stride) {
+__device__ __forceinline__ uint32_t dma_lane_offset_at(int lane, int R0, int row_stride) {
   constexpr int CH = D / 8;
-  constexpr int ROWS_PER_KB = 1024 / (D * 2);
-  const int row = ROWS_PER_KB * wave + lane / CH;
+  const int row = R0 + lane / CH;
   const int c = (lane % CH) ^ swz<CH>(row);
   return (uint32_t)(row * row_stride + c * 16);
+}
+template <int D>
+__device__ __forceinline__ uint32_t dma_lane_offset(int lane, int wave, int row_stride) {
+  return dma_lane_offset_at<D>(lane, (1024 / (D * 2)) * wave, row_stride);
 }
 
 // Bytes of a tile's rows [0, min(n_in, BN)) when rows are `row_stride` apart
@@ -300,18 +303,21 @@ __device__ __forceinline__ int tile_bytes(int n_in, int row_stride, int row_byte
 // One KV tile of K (or bf16 V) starting at `tile` (its first row), rows
 // `row_stride` bytes apart; rows >= n_in are zero-filled.  One buffer resource
 // per tile; the instructions differ only in their VGPR offset and LDS target.
+// With D = 256 an instruction covers 2 rows and R0 moves by 8 rows, which
+// changes swz(): there every instruction's offset is formed afresh.
 template <int D>
 __device__ __forceinline__ void dma_tile(const char* tile, int row_stride, int n_in, char* lds_tile, int wave,
-                                         uint32_t lane_off) {
+                                         int lane, uint32_t lane_off) {
   constexpr int ROWB = D * 2;
   constexpr int ROWS_PER_KB = 1024 / ROWB;
   constexpr int PER_WAVE = BN * ROWB / (NWAVES * 1024);
+  constexpr bool SAME_SWZ = (ROWS_PER_KB * NWAVES) % 16 == 0;
   const u32x4 rs = rsrc_words(tile, tile_bytes(n_in, row_stride, ROWB));
   const uint32_t step = (uint32_t)(ROWS_PER_KB * NWAVES * row_stride);
 #pragma unroll
   for (int r = 0; r < PER_WAVE; ++r) {
     const int R0 = ROWS_PER_KB * (NWAVES * r + wave);
-    dma16(rs, lds_tile + R0 * ROWB, lane_off + r * step);
+    dma16(rs, lds_tile + R0 * ROWB, SAME_SWZ ? lane_off + r * step : dma_lane_offset_at<D>(lane, R0, row_stride));
   }
 }
 
@@ -335,8 +341,11 @@ __device__ __forceinline__ Params reread_args() {
 // the second, both through the same code with their own LDS stages, and
 // group 1 hands its partial state to group 0 through LDS at the end (the
 // launch for row blocks that fit the CUs once; no workspace, no queue).
+// D = 256 holds 128 accumulator registers per lane and runs one workgroup per
+// CU (one wave per SIMD); the other head dims run two.
 template <int D, bool FP16, bool V_FP8, bool KV, int KSPLIT>
-__global__ void __launch_bounds__(NTHREADS * KSPLIT, KSPLIT == 1 ? 2 : 1) attn_fwd_kernel(const Params args) {
+__global__ void __launch_bounds__(NTHREADS * KSPLIT, (KSPLIT == 1 && D <= 128) ? 2 : 1)
+    attn_fwd_kernel(const Params args) {
   constexpr int CH = D / 8;              // 16-byte chunks per row (8 elements)
   constexpr int ROWB = D * 2;            // bytes per row of a K/V tile in LDS
   constexpr int KSTEPS = D / 16;         // k-steps of S^T = K.Q^T
@@ -345,10 +354,13 @@ __global__ void __launch_bounds__(NTHREADS * KSPLIT, KSPLIT == 1 ? 2 : 1) attn_f
   constexpr int SLABS = BN / 16;         // k-slabs of O^T = V^T.P^T
   constexpr int TILE_BYTES = BN * ROWB;
   constexpr int CH8 = D / 16;            // 16-byte chunks per fp8 row
-  constexpr int F8_LOADS = BN * D / (NTHREADS * 16);
+  constexpr int F8_CHUNKS = BN * CH8;     // 16-byte chunks of an fp8 V tile
+  // 16-byte fp8 loads per thread (D = 32: half the threads load one chunk each)
+  constexpr int F8_LOADS = (F8_CHUNKS + NTHREADS - 1) / NTHREADS;
   constexpr float TAU = 8.0f;            // rescale only when a row max grows by more than 2^8
   static_assert(NBLK == 2, "the S^T code below holds two 32-key blocks");
-  static_assert(F8_LOADS >= 1 && F8_LOADS * NTHREADS * 16 == BN * D, "fp8 tile split");
+  static_assert(D == 32 || D == 64 || D == 128 || D == 256, "head dims 32, 64, 128, 256");
+  static_assert(F8_LOADS * NTHREADS == F8_CHUNKS || F8_CHUNKS < NTHREADS, "fp8 tile split");
   static_assert(BN == 64, "one key_valid byte per lane of wave 0");
 
   static_assert(KSPLIT == 1 || KSPLIT == 2, "one or two groups of waves");
@@ -497,7 +509,7 @@ __global__ void __launch_bounds__(NTHREADS * KSPLIT, KSPLIT == 1 ? 2 : 1) attn_f
       char* kd = kst[stage];
       char* vdst = vst[stage];
       if (seg0) {
-        dma_tile<D>(kcb + (int64_t)row0 * kcs, kcs, n_in, kd, wave, koff_c);
+        dma_tile<D>(kcb + (int64_t)row0 * kcs, kcs, n_in, kd, wave, lane, koff_c);
         if constexpr (V_FP8) {
           const char* tb = vcb + (int64_t)row0 * vcs;
           const auto rs = make_rsrc(tb, tile_bytes(n_in, vcs, D));
@@ -505,15 +517,16 @@ __global__ void __launch_bounds__(NTHREADS * KSPLIT, KSPLIT == 1 ? 2 : 1) attn_f
           for (int i = 0; i < F8_LOADS; ++i) {
             const int qd = i * NTHREADS + tid;
             const int row = qd / CH8, c16 = qd % CH8;
-            f8reg[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                      rs, (uint32_t)(row * vcs + c16 * 16), 0, 0));
+            if (F8_CHUNKS >= NTHREADS || qd < F8_CHUNKS)
+              f8reg[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                        rs, (uint32_t)(row * vcs + c16 * 16), 0, 0));
           }
         } else {
-          dma_tile<D>(vcb + (int64_t)row0 * vcs, vcs, n_in, vdst, wave, voff_c);
+          dma_tile<D>(vcb + (int64_t)row0 * vcs, vcs, n_in, vdst, wave, lane, voff_c);
         }
       } else {
-        dma_tile<D>(knb + (int64_t)row0 * kns, kns, n_in, kd, wave, koff_new);
-        dma_tile<D>(vnb + (int64_t)row0 * vns, vns, n_in, vdst, wave, voff_new);
+        dma_tile<D>(knb + (int64_t)row0 * kns, kns, n_in, kd, wave, lane, koff_new);
+        dma_tile<D>(vnb + (int64_t)row0 * vns, vns, n_in, vdst, wave, lane, voff_new);
       }
       if constexpr (KV) {
         // one byte per thread so that bytes past the segment end read as 0
@@ -621,6 +634,7 @@ __global__ void __launch_bounds__(NTHREADS * KSPLIT, KSPLIT == 1 ? 2 : 1) attn_f
           for (int i = 0; i < F8_LOADS; ++i) {
             const int qd = i * NTHREADS + tid;
             const int row = qd / CH8, c16 = qd % CH8;
+            if (F8_CHUNKS < NTHREADS && qd >= F8_CHUNKS) continue;
             const u32x4 w = f8reg[i];
             const u32x4 lo = dequant_fp8x8(w.x, w.y, vsc);  // elements 16*c16 .. +7
             const u32x4 hi = dequant_fp8x8(w.z, w.w, vsc);  // elements 16*c16+8 .. +15
@@ -1035,8 +1049,32 @@ kernel_fn pick_kernel(bool fp16, bool vfp8) {
 // of its code (the tile loop is then the same as with no mask support at all)
 template <int D>
 kernel_fn pick_kernel(bool fp16, bool vfp8, bool kv, bool two_groups) {
-  if (two_groups) return kv ? pick_kernel<D, true, 2>(fp16, vfp8) : pick_kernel<D, false, 2>(fp16, vfp8);
+  if constexpr (D <= 128) {
+    if (two_groups) return kv ? pick_kernel<D, true, 2>(fp16, vfp8) : pick_kernel<D, false, 2>(fp16, vfp8);
+  }
   return kv ? pick_kernel<D, true, 1>(fp16, vfp8) : pick_kernel<D, false, 1>(fp16, vfp8);
+}
+
+// The two-group form needs two groups' LDS stages in one workgroup (256 KiB
+// at D = 256, more than a CU holds): not at D = 256.
+inline bool two_group_dim(int64_t D) { return D <= 128; }
+
+kernel_fn pick_kernel_d(int64_t D, bool fp16, bool vfp8, bool kv, bool two_groups) {
+  switch (D) {
+    case 32: return pick_kernel<32>(fp16, vfp8, kv, two_groups);
+    case 64: return pick_kernel<64>(fp16, vfp8, kv, two_groups);
+    case 128: return pick_kernel<128>(fp16, vfp8, kv, two_groups);
+    default: return pick_kernel<256>(fp16, vfp8, kv, false);
+  }
+}
+
+int slot_bytes_d(int64_t D) {
+  switch (D) {
+    case 32: return slot_bytes<32>();
+    case 64: return slot_bytes<64>();
+    case 128: return slot_bytes<128>();
+    default: return slot_bytes<256>();
+  }
 }
 
 inline bool aligned_to(const void* ptr, uintptr_t a) { return (reinterpret_cast<uintptr_t>(ptr) % a) == 0; }
@@ -1060,9 +1098,9 @@ int schedule_one(int64_t Lmax, int64_t P, int64_t SN, bool has_cache) {
 }
 
 // Workgroups one XCD of the current device holds at once for kernel `which`
-// (0..11, see pick_index): occupancy per CU x CUs / XCDs, cached per device.
+// (0..23, see pick_index): occupancy per CU x CUs / XCDs, cached per device.
 constexpr int MAX_DEVICES = 64;
-std::atomic<int> g_slots[MAX_DEVICES][12];
+std::atomic<int> g_slots[MAX_DEVICES][24];
 std::atomic<int> g_xcds[MAX_DEVICES];
 std::atomic<int> g_cus[MAX_DEVICES];
 
@@ -1097,7 +1135,8 @@ int device_xcds() {
 }
 
 int pick_index(int D, bool fp16, bool vfp8, bool kv) {
-  return 2 * ((D == 128 ? 3 : 0) + (fp16 ? 1 : (vfp8 ? 2 : 0))) + (kv ? 1 : 0);
+  const int di = D == 32 ? 0 : D == 64 ? 1 : D == 128 ? 2 : 3;
+  return 2 * (3 * di + (fp16 ? 1 : (vfp8 ? 2 : 0))) + (kv ? 1 : 0);
 }
 
 int slots_per_xcd(kernel_fn fn, int which, int* out) {
@@ -1144,8 +1183,8 @@ int plan_launch(const qik_attn_args* a, bool split, Launch* L) {
   const bool fp16 = a->dtype == QIK_DTYPE_FP16;
   const bool vfp8 = (a->flags & QIK_V_CACHE_FP8) != 0;
   const bool kv = (a->flags & QIK_HAS_KEY_VALID) != 0;
-  L->fn = (a->D == 128) ? pick_kernel<128>(fp16, vfp8, kv, false) : pick_kernel<64>(fp16, vfp8, kv, false);
-  L->slot = (a->D == 128) ? slot_bytes<128>() : slot_bytes<64>();
+  L->fn = pick_kernel_d(a->D, fp16, vfp8, kv, false);
+  L->slot = slot_bytes_d(a->D);
   L->ws_bytes = 0;
   L->ctl_bytes = 0;
   L->grid = 0;
@@ -1154,10 +1193,10 @@ int plan_launch(const qik_attn_args* a, bool split, Launch* L) {
   if (n == 0) return QIK_OK;
   const int nx = device_xcds();
   int sx = 1;
-  if (split && n <= device_cus()) {
+  if (split && two_group_dim(a->D) && n <= device_cus()) {
     // row blocks fit the CUs once: one two-group workgroup per row block, its
     // KV tiles split between the groups and merged in LDS (no workspace)
-    L->fn = (a->D == 128) ? pick_kernel<128>(fp16, vfp8, kv, true) : pick_kernel<64>(fp16, vfp8, kv, true);
+    L->fn = pick_kernel_d(a->D, fp16, vfp8, kv, true);
     L->threads = 2 * NTHREADS;
     L->plan = make_plan((int)n, (int)nmb, 1, 0, 1, nx);
     L->grid = (int64_t)nx * L->plan.wpx;
@@ -1262,7 +1301,7 @@ const char* qik_strerror(int status) {
     case QIK_ERR_NULL_ARG: return "a required pointer is NULL";
     case QIK_ERR_ABI_VERSION: return "qik_attn_args.abi_version does not match the library";
     case QIK_ERR_DTYPE: return "fp16/bf16 only";
-    case QIK_ERR_HEAD_DIM: return "head_dim must be 64 or 128";
+    case QIK_ERR_HEAD_DIM: return "head_dim must be 32, 64, 128 or 256";
     case QIK_ERR_SHAPE: return "negative or oversized B/SQ/SN/P/H";
     case QIK_ERR_CACHE: return "cache flag, P and cache pointers are inconsistent";
     case QIK_ERR_FP8_SCALE: return "fp8 cache V needs the cache, a v_scale pointer and bf16 q/k/v";
@@ -1287,7 +1326,7 @@ int qik_attn_validate(const qik_attn_args* a) {
   if (a == nullptr) return QIK_ERR_NULL_ARG;
   if (a->abi_version != QIK_ABI_VERSION || a->reserved0 != 0 || a->reserved1 != 0) return QIK_ERR_ABI_VERSION;
   if (a->dtype != QIK_DTYPE_BF16 && a->dtype != QIK_DTYPE_FP16) return QIK_ERR_DTYPE;
-  if (a->D != 64 && a->D != 128) return QIK_ERR_HEAD_DIM;
+  if (a->D != 32 && a->D != 64 && a->D != 128 && a->D != 256) return QIK_ERR_HEAD_DIM;
   const int64_t lim = (int64_t)INT_MAX;
   if (a->B < 0 || a->SQ < 0 || a->SN < 0 || a->P < 0 || a->H < 0) return QIK_ERR_SHAPE;
   if (a->SQ > lim || a->SN > lim || a->P > lim || a->H > lim || a->P + a->SN > lim) return QIK_ERR_SHAPE;

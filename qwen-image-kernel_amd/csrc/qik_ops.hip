@@ -463,6 +463,10 @@ inline bool strides_ok(const int64_t st[3], int64_t mult) {
   return st[0] % mult == 0 && st[1] % mult == 0 && st[2] % mult == 0;
 }
 
+// Head dims of these kernels: 32, 64, 128, 256 (the attention kernel's).
+inline bool head_dim_ok(int64_t D) { return D == 32 || D == 64 || D == 128 || D == 256; }
+inline int head_dim_index(int64_t D) { return D == 32 ? 0 : D == 64 ? 1 : D == 128 ? 2 : 3; }
+
 inline bool sizes_ok(int64_t a, int64_t b, int64_t c, int64_t d) {
   if (a < 0 || b < 0 || c < 0 || d < 0) return false;
   const int64_t lim = (int64_t)INT_MAX;
@@ -478,7 +482,7 @@ int qik_rms_rope(const qik_rms_rope_args* a, void* stream) {
   if (a == nullptr) return QIK_ERR_NULL_ARG;
   if (a->abi_version != QIK_ABI_VERSION || a->reserved0 != 0) return QIK_ERR_ABI_VERSION;
   if (a->dtype != QIK_DTYPE_BF16 && a->dtype != QIK_DTYPE_FP16) return QIK_ERR_DTYPE;
-  if (a->D != 64 && a->D != 128) return QIK_ERR_HEAD_DIM;
+  if (!head_dim_ok(a->D)) return QIK_ERR_HEAD_DIM;
   if (!sizes_ok(a->B, a->S, a->H, a->D)) return QIK_ERR_SHAPE;
   const int64_t rows = a->B * a->S * a->H;
   if (rows == 0) return QIK_OK;
@@ -509,9 +513,12 @@ int qik_rms_rope(const qik_rms_rope_args* a, void* stream) {
   const int rpb = NTHREADS / (int)(a->D / 8) * RR;
   const int64_t grid = (rows + rpb - 1) / rpb;
   if (grid > (int64_t)UINT_MAX) return QIK_ERR_SHAPE;
-  const void* fn;
-  if (a->D == 128) fn = fp16 ? (const void*)rms_rope_kernel<128, true> : (const void*)rms_rope_kernel<128, false>;
-  else fn = fp16 ? (const void*)rms_rope_kernel<64, true> : (const void*)rms_rope_kernel<64, false>;
+  const void* const fns[4][2] = {
+      {(const void*)rms_rope_kernel<32, false>, (const void*)rms_rope_kernel<32, true>},
+      {(const void*)rms_rope_kernel<64, false>, (const void*)rms_rope_kernel<64, true>},
+      {(const void*)rms_rope_kernel<128, false>, (const void*)rms_rope_kernel<128, true>},
+      {(const void*)rms_rope_kernel<256, false>, (const void*)rms_rope_kernel<256, true>}};
+  const void* fn = fns[head_dim_index(a->D)][fp16 ? 1 : 0];
   void* kargs[] = {&p};
   const hipError_t e =
       hipLaunchKernel(fn, dim3((unsigned)grid), dim3(NTHREADS), kargs, 0, static_cast<hipStream_t>(stream));
@@ -529,7 +536,7 @@ int validate_store(const qik_slab_store_args* a, int64_t* rows) {
   if (a->dtype != QIK_DTYPE_BF16 && a->dtype != QIK_DTYPE_FP16) return QIK_ERR_DTYPE;
   const bool fp8 = a->v_fp8 != 0;
   if (fp8 != (a->v_scale != nullptr)) return QIK_ERR_FP8_SCALE;
-  if (a->D != 64 && a->D != 128) return QIK_ERR_HEAD_DIM;
+  if (!head_dim_ok(a->D)) return QIK_ERR_HEAD_DIM;
   if (!sizes_ok(a->B, a->P, a->H, a->D)) return QIK_ERR_SHAPE;
   *rows = a->B * a->H * a->P;
   if (*rows == 0) return QIK_OK;
@@ -597,11 +604,12 @@ int store(const qik_slab_store_args* a, float* partial, hipStream_t s) {
   void* qargs[] = {&qp};
   // the fp8 kernels per head size and source type (bf16 or fp16 V)
   const bool f16 = a->dtype == QIK_DTYPE_FP16;
-  const int kix = (a->D == 128 ? 0 : 2) + (f16 ? 1 : 0);
-  const void* const quant_fns[4] = {(const void*)slab_quant_fp8_kernel<128, false>,
-                                    (const void*)slab_quant_fp8_kernel<128, true>,
-                                    (const void*)slab_quant_fp8_kernel<64, false>,
-                                    (const void*)slab_quant_fp8_kernel<64, true>};
+  const int kix = 2 * head_dim_index(a->D) + (f16 ? 1 : 0);
+  const void* const quant_fns[8] = {
+      (const void*)slab_quant_fp8_kernel<32, false>,  (const void*)slab_quant_fp8_kernel<32, true>,
+      (const void*)slab_quant_fp8_kernel<64, false>,  (const void*)slab_quant_fp8_kernel<64, true>,
+      (const void*)slab_quant_fp8_kernel<128, false>, (const void*)slab_quant_fp8_kernel<128, true>,
+      (const void*)slab_quant_fp8_kernel<256, false>, (const void*)slab_quant_fp8_kernel<256, true>};
   const void* fq = quant_fns[kix];
 
   if (fp8 && partial != nullptr) {
@@ -614,10 +622,11 @@ int store(const qik_slab_store_args* a, float* partial, hipStream_t s) {
     if (ncopy + heads * chunks > (int64_t)INT_MAX) return QIK_ERR_SHAPE;
     int nc = (int)ncopy;
     void* args2[] = {&cp, &qp, &nc};
-    const void* const copy_scale_fns[4] = {(const void*)slab_copy_scale_kernel<128, false>,
-                                           (const void*)slab_copy_scale_kernel<128, true>,
-                                           (const void*)slab_copy_scale_kernel<64, false>,
-                                           (const void*)slab_copy_scale_kernel<64, true>};
+    const void* const copy_scale_fns[8] = {
+        (const void*)slab_copy_scale_kernel<32, false>,  (const void*)slab_copy_scale_kernel<32, true>,
+        (const void*)slab_copy_scale_kernel<64, false>,  (const void*)slab_copy_scale_kernel<64, true>,
+        (const void*)slab_copy_scale_kernel<128, false>, (const void*)slab_copy_scale_kernel<128, true>,
+        (const void*)slab_copy_scale_kernel<256, false>, (const void*)slab_copy_scale_kernel<256, true>};
     const void* fc = copy_scale_fns[kix];
     if (hipLaunchKernel(fc, dim3((unsigned)(ncopy + heads * chunks)), dim3(QTHREADS), args2, 0, s) != hipSuccess)
       return QIK_ERR_LAUNCH;
@@ -630,10 +639,11 @@ int store(const qik_slab_store_args* a, float* partial, hipStream_t s) {
                                  dim3(NTHREADS), cargs, 0, s);
   if (e != hipSuccess) return QIK_ERR_LAUNCH;
   if (!fp8) return QIK_OK;
-  const void* const scale_fns[4] = {(const void*)slab_scale_fp8_kernel<128, false>,
-                                    (const void*)slab_scale_fp8_kernel<128, true>,
-                                    (const void*)slab_scale_fp8_kernel<64, false>,
-                                    (const void*)slab_scale_fp8_kernel<64, true>};
+  const void* const scale_fns[8] = {
+      (const void*)slab_scale_fp8_kernel<32, false>,  (const void*)slab_scale_fp8_kernel<32, true>,
+      (const void*)slab_scale_fp8_kernel<64, false>,  (const void*)slab_scale_fp8_kernel<64, true>,
+      (const void*)slab_scale_fp8_kernel<128, false>, (const void*)slab_scale_fp8_kernel<128, true>,
+      (const void*)slab_scale_fp8_kernel<256, false>, (const void*)slab_scale_fp8_kernel<256, true>};
   const void* fs = scale_fns[kix];
   e = hipLaunchKernel(fs, dim3((unsigned)(heads * chunks)), dim3(QTHREADS), qargs, 0, s);
   if (e != hipSuccess) return QIK_ERR_LAUNCH;

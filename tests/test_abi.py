@@ -113,6 +113,8 @@ def test_validate_accepts_reference_call_patterns():
         (lambda a: setattr(a, "reserved0", 1), -2),
         (lambda a: setattr(a, "dtype", 7), -3),              # triton_attention.py:190
         (lambda a: setattr(a, "D", 96), -4),
+        (lambda a: setattr(a, "D", 16), -4),
+        (lambda a: setattr(a, "D", 512), -4),
         (lambda a: setattr(a, "SQ", -1), -5),
         (lambda a: setattr(a, "flags", 64), -5),
         (lambda a: setattr(a, "P", 16), -6),                 # P > 0 without HAS_CACHE (:192-196)
@@ -246,7 +248,7 @@ def _store_args(**kw):
 
 
 @pytest.mark.parametrize("kw,code", [
-    (dict(abi_version=0), -2), (dict(dtype=9), -3), (dict(D=32), -4), (dict(P=-1), -5),
+    (dict(abi_version=0), -2), (dict(dtype=9), -3), (dict(D=96), -4), (dict(P=-1), -5),
     (dict(v_scale=None), -7),                     # fp8 V needs the scale output
     (dict(v_fp8=0), -7),                          # a scale output without fp8 V
     (dict(k=None), -1), (dict(v_dst=0x10004), -8), (dict(stride_k=_lib._i64x3(8192, 260, 128)), -8),
@@ -261,7 +263,7 @@ def test_slab_store_without_rows_is_a_no_op():
 
 
 @pytest.mark.parametrize("kw,code", [
-    (dict(abi_version=0), -2), (dict(dtype=9), -3), (dict(D=32), -4), (dict(P=-1), -5),
+    (dict(abi_version=0), -2), (dict(dtype=9), -3), (dict(D=96), -4), (dict(P=-1), -5),
     (dict(v_scale=None), -7), (dict(v_fp8=0), -7),
     (dict(k=None), -1), (dict(v_dst=0x10004), -8),
 ])

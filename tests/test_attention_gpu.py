@@ -276,7 +276,7 @@ def test_decode_fp8_slab_head_dim_64_ragged_with_key_valid():
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("D", [32, 64, 128, 256])
 def test_dtypes_and_head_dims(dtype, D):
     _flush(f"case dtype={dtype} D={D}")
     segs, S = ol.make_segments([("text", 37), ("img", 16), ("text", 11), ("img", 25)])
@@ -287,6 +287,39 @@ def test_dtypes_and_head_dims(dtype, D):
     out = qik.block_causal_flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), torch.from_numpy(L).to(DEV), None)
     assert out.dtype == dtype
     _check(out, oa.attention_fp32(q, k, v, L), what=f"{dtype} D={D}")
+
+
+@pytest.mark.parametrize("D", [32, 256])
+def test_other_head_dims_slab_fp8_key_valid_and_long_rows(D):
+    """Head dims 32 and 256 (the reference kernel takes any power-of-two
+    HEAD_DIM, triton_attention.py:63-74): an fp8 slab with ragged lengths and
+    padded keys, and a fresh-key call long enough for several rounds of row
+    blocks (the queued launch and its merged pieces; the two-group form for
+    D = 32), against the fp32 oracle."""
+    _flush(f"case head dim {D}: fp8 slab + key_valid, long rows")
+    g = torch.Generator().manual_seed(900 + D)
+    B, P, SN, H = 2, 200, 130, 3
+    kp, vp = (_rand((B, P, H, D), g) for _ in range(2))
+    cache = qik.ContiguousKVCache(1, B, P + 40, H, D, v_fp8=True, device=DEV)
+    cache.get_layer(0).store(kp.to(DEV), vp.to(DEV))
+    k8, v8, sc = cache.get_layer(0).views()
+    q, kn, vn = (_rand((B, SN, H, D), g) for _ in range(3))
+    L = (np.arange(SN, dtype=np.int32) + P).clip(max=P + SN - 1)
+    L[:40] = P - 1 - np.arange(40)
+    kv = torch.ones(B, P + SN, dtype=torch.bool)
+    kv[1, 5:30] = False
+    kv[0, P + 7:P + 9] = False
+    out = qik.block_causal_flash_attention(q.to(DEV), kn.to(DEV), vn.to(DEV), torch.from_numpy(L).to(DEV),
+                                           kv.to(DEV), cache_k=k8, cache_v=v8, cache_v_scale=sc)
+    _check(out, oa.attention_fp32(q, kn, vn, L, kv, k8.cpu(), v8.cpu(), sc.cpu()), what=f"fp8 slab D={D}")
+    for split in (True, False):
+        S, H2 = 2100, 6
+        segs, S0 = ol.make_segments([("text", 100), ("img", 1500)])
+        qq, kk, vv = (_rand((1, S, H2, D), g) for _ in range(3))
+        L2 = ol.build_prefix_lengths(segs, S0, S)
+        out = qik.block_causal_flash_attention(qq.to(DEV), kk.to(DEV), vv.to(DEV), torch.from_numpy(L2).to(DEV),
+                                               None, split_tail=split)
+        _check(out, oa.attention_fp32(qq, kk, vv, L2, None, heads=range(H2)), what=f"long rows D={D} split={split}")
 
 
 def test_fused_qkv_strided_value_view():

@@ -61,6 +61,8 @@ def _rope_oracle(x, w, freqs, eps, dtype="bf16"):
     (1, 65, 3, 128, torch.float16),
     (2, 9, 1, 128, torch.bfloat16),      # one head: a thread's next row is 16 positions on
     (4, 3, 2, 128, torch.bfloat16),      # 16 rows on crosses whole batches (b carry)
+    (1, 70, 6, 32, torch.bfloat16),      # the other head dims
+    (2, 33, 3, 256, torch.float16),
 ])
 def test_rms_rope_bit_exact_vs_oracle(B, S, H, D, dtype):
     _flush(f"case rms_rope {B}x{S}x{H}x{D} {dtype}")
@@ -111,7 +113,8 @@ def _torch_store(k, v, v_fp8):
 
 
 @pytest.mark.parametrize("B,P,H,D,v_fp8", [(1, 2560, 24, 128, True), (2, 333, 5, 128, True),
-                                           (1, 100, 3, 64, True), (2, 257, 4, 128, False)])
+                                           (1, 100, 3, 64, True), (2, 257, 4, 128, False),
+                                           (2, 150, 3, 32, True), (1, 90, 2, 256, True), (1, 65, 2, 256, False)])
 def test_slab_store_bit_exact_vs_torch_ops(B, P, H, D, v_fp8):
     _flush(f"case slab store B={B} P={P} H={H} D={D} fp8={v_fp8}")
     g = torch.Generator().manual_seed(P + H)
