@@ -28,7 +28,8 @@ MLP-in and MLP-out shapes (4352 tokens, H*D = 3072) and at the text stream's
 fused QKV and MLP-out (256 tokens): GEMM device time, TFLOP/s against
 the 5.0 PF dense fp8 peak, the activation quantiser's time, the whole
 FP8Linear call through the Python API, torch._scaled_mm (hipBLASLt, the call
-the reference makes) on the same device for context, and an fp32 matmul of the
+the reference makes) on the same device, timed in batches alternating with the
+GEMM's (medians), and an fp32 matmul of the
 dequantised operands on the host CPU for the reference shape.
 """
 
@@ -369,6 +370,21 @@ def _batch_us(fn, reps: int) -> float:
     return e0.elapsed_time(e1) / reps * 1e3
 
 
+def _interleaved_us(fns: dict, reps: int, rounds: int) -> dict:
+    """Device time per call of each fn, measured in alternating batches (the
+    order reversed every round, so no fn always runs first after the others),
+    median over the rounds: kernels compared under the same clock and cache
+    state."""
+    import statistics
+
+    times = {k: [] for k in fns}
+    items = list(fns.items())
+    for r in range(rounds):
+        for k, fn in (items if r % 2 == 0 else items[::-1]):
+            times[k].append(_batch_us(fn, reps))
+    return {k: statistics.median(v) for k, v in times.items()}
+
+
 def _host_us(fn, reps: int) -> float:
     """Host (wall) time per call of fn() in a loop that only issues work: the
     device runs behind and is synchronised once, after the loop."""
@@ -515,7 +531,17 @@ def fp8_linear_ops(qik, dev, with_cpu: bool) -> dict:
         gneed = ctypes.c_int64(0)
         _lib.check(lib.qik_fp8_gemm_workspace_size(ctypes.byref(a), ctypes.byref(gneed)), "workspace size")
         gws = torch.empty(max(gneed.value // 4, 4), dtype=torch.float32, device=dev)
-        us = _batch_us(lambda: lib.qik_fp8_gemm_ws(ctypes.byref(a), gws.data_ptr(), gneed.value, stream), 30)
+        fns = {"ours": lambda: lib.qik_fp8_gemm_ws(ctypes.byref(a), gws.data_ptr(), gneed.value, stream)}
+        try:
+            wt = fq.weight.t()
+            torch._scaled_mm(xq, wt, scale_a=sa, scale_b=fq.weight_scale, out_dtype=torch.bfloat16)
+            fns["torch"] = lambda: torch._scaled_mm(xq, wt, scale_a=sa, scale_b=fq.weight_scale,
+                                                    out_dtype=torch.bfloat16)
+            sm_err = None
+        except (RuntimeError, NotImplementedError) as e:
+            sm_err = f"unavailable: {type(e).__name__}"
+        med = _interleaved_us(fns, 10, 6)
+        us = med["ours"]
         qa = f8.quant_args(x.reshape(-1), xq, sa, _lib.FP8_ACTIVATION)
         nws = ctypes.c_int64()
         _lib.check(lib.qik_fp8_quant_workspace_size(ctypes.byref(qa), ctypes.byref(nws)), "workspace size")
@@ -531,13 +557,8 @@ def fp8_linear_ops(qik, dev, with_cpu: bool) -> dict:
                  "quantize_us": round(q_us, 2),
                  "quantize_gbs": round(M * K * 3 / (q_us * 1e-6) / 1e9, 1), "api_us": round(api_us, 2),
                  "host_us": round(host_us, 2)}
-        try:
-            wt = fq.weight.t()
-            sm_us = _batch_us(lambda: torch._scaled_mm(xq, wt, scale_a=sa, scale_b=fq.weight_scale,
-                                                       out_dtype=torch.bfloat16), 30)
-            entry["torch_scaled_mm_us"] = round(sm_us, 2)
-        except (RuntimeError, NotImplementedError) as e:
-            entry["torch_scaled_mm_us"] = f"unavailable: {type(e).__name__}"
+        entry["torch_scaled_mm_us"] = round(med["torch"], 2) if sm_err is None else sm_err
+        entry["timing"] = "medians of 6 alternating batches of 10 back-to-back launches, ours and torch._scaled_mm"
         if with_cpu and M == 1536:
             xd = (xq.float() * sa).cpu()
             wd = (fq.weight.float() * fq.weight_scale).cpu()
