@@ -29,6 +29,7 @@
 #include <algorithm>
 #include <cmath>
 #include <thread>
+#include <type_traits>
 #include <utility>
 #include <vector>
 
@@ -504,6 +505,7 @@ struct GemmParams {
 
 template <int BM_, int BN_, int NS_, int WGM_ = 2, int WGN_ = 2>
 struct Cfg {
+  static constexpr int KB = qik_fp8::KB;
   static constexpr int BM = BM_, BN = BN_, NS = NS_;
   static constexpr int WGM = WGM_, WGN = WGN_;     // waves along m and n
   static constexpr int NW = WGM * WGN, NT = 64 * NW;
@@ -518,6 +520,28 @@ struct Cfg {
   static_assert(AI * 16 * NW == BM && WI * 16 * NW == BN, "whole copies per wave");
   static_assert(MI * 32 == WM && NJ * 32 == WN, "whole MFMA blocks per wave");
   static_assert(NS >= 3, "copies run at least two stages ahead");
+};
+
+// Tiles with 128 k-bytes per stage: two MFMA k-steps per barrier, and each
+// copied row a whole 128-byte line (at 64 bytes a row is half a line, fetched
+// by two stages).  Two stages: a stage's copies go out one step (two MFMA
+// k-steps) before its first fragment reads.
+template <int BM_, int BN_, int WGM_ = 2, int WGN_ = 4>
+struct CfgK128 {
+  static constexpr int KB = 128, NS = 2;
+  static constexpr int BM = BM_, BN = BN_;
+  static constexpr int WGM = WGM_, WGN = WGN_;
+  static constexpr int NW = WGM * WGN, NT = 64 * NW;
+  static constexpr int WM = BM / WGM, WN = BN / WGN;
+  static constexpr int MI = WM / 32, NJ = WN / 32;
+  static constexpr int A_BYTES = BM * KB;
+  static constexpr int STAGE = (BM + BN) * KB;
+  static constexpr int AI = BM / (8 * NW);  // 1 KiB copies (8 rows) of A per wave per stage
+  static constexpr int WI = BN / (8 * NW);
+  static constexpr int COPIES = AI + WI;
+  static_assert(NW == 4 || NW == 8, "one or two waves per SIMD");
+  static_assert(AI * 8 * NW == BM && WI * 8 * NW == BN, "whole copies per wave");
+  static_assert(MI * 32 == WM && NJ * 32 == WN, "whole MFMA blocks per wave");
 };
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
@@ -555,8 +579,33 @@ __device__ __forceinline__ void wait_vmcnt() {
 // contiguous KiB.
 __device__ __forceinline__ int swz(int r) { return (r >> 2) & 3; }
 
-// One BM x BN output tile of region g; bx counts the region's workgroups
-// (bx % 8 is the XCD: every region starts at a multiple of 8).
+// Origin of the tile of workgroup bx of region rg (bx % 8 is the XCD: every
+// region starts at a multiple of 8): XCD x takes a contiguous run of the tile
+// order, which walks group_m tile rows at a time.  False for a padding
+// workgroup.
+template <class C>
+__device__ __forceinline__ bool tile_origin(const GemmRegion& rg, const int bx, int& m0, int& n0) {
+  const int T = rg.ntm * rg.ntn;
+  const int x = bx & 7, s = bx >> 3;
+  const int q = T >> 3, r = T & 7;
+  if (s >= q + (x < r ? 1 : 0)) return false;
+  const int t = x * q + min(x, r) + s;
+  const int gsz_full = rg.group_m * rg.ntn;
+  const int g = t / gsz_full;
+  const int first = g * rg.group_m;
+  const int gm = min(rg.group_m, rg.ntm - first);
+  const int tr = t - g * gsz_full;
+  m0 = (first + tr % gm) * C::BM;
+  n0 = (tr / gm) * C::BN;
+  return true;
+}
+
+template <class C, bool FP16>
+__device__ __forceinline__ void store_tile(const GemmParams& p, const GemmRegion& rg, const int m0, const int n0,
+                                           const f32x16 (&acc)[C::NJ][C::MI], unsigned char* lds, const int wave,
+                                           const int lane);
+
+// One BM x BN output tile of region g; bx counts the region's workgroups.
 // SPLIT: the workgroup sums k-steps [kb, ke) of slice `slice` and writes the
 // fp32 sums to p.partial instead of the outputs.
 template <class C, bool FP16, bool SPLIT = false>
@@ -567,21 +616,8 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, const GemmRegion&
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: copy targets go to SGPRs
   const int wm = wave % C::WGM, wn = wave / C::WGM;
 
-  // tile of this workgroup: XCD x takes a contiguous run of the tile order,
-  // which walks group_m tile rows at a time; the padding workgroups leave
-  const int T = rg.ntm * rg.ntn;
-  const int x = bx & 7, s = bx >> 3;
-  const int q = T >> 3, r = T & 7;
-  if (s >= q + (x < r ? 1 : 0)) return;
-  const int t = x * q + min(x, r) + s;
-  const int gsz_full = rg.group_m * rg.ntn;
-  const int g = t / gsz_full;
-  const int first = g * rg.group_m;
-  const int gm = min(rg.group_m, rg.ntm - first);
-  const int tr = t - g * gsz_full;
-  const int tm = first + tr % gm;
-  const int tn = tr / gm;
-  const int m0 = tm * C::BM, n0 = tn * C::BN;
+  int m0, n0;
+  if (!tile_origin<C>(rg, bx, m0, n0)) return;
   const int mrows = min(C::BM, p.M - m0);
   const int nrows = min(C::BN, rg.N - n0);
 
@@ -722,16 +758,6 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, const GemmRegion&
   }
   if (kt < nk) step(kt, 0);
 
-  // epilogue: out[m][n..n+3] = round(acc * (sa * sw) + bias[n..n+3]),
-  // staged through LDS: a lane's results are 4 columns of one row, so stored
-  // straight from the accumulators every store instruction would touch 32
-  // rows; from LDS each one writes whole rows of the tile (64 lanes x 16 B).
-  // Staged row ml keeps its 16-byte chunk c at physical chunk c ^ (ml % CPR),
-  // which spreads a fragment's 32 rows over the banks.
-  constexpr int RB = C::BN * 2;   // bytes of a staged row
-  constexpr int CPR = RB / 16;    // 16-byte chunks per row
-  constexpr int RPI = 64 / CPR;   // rows per store instruction
-  static_assert(C::BM * RB <= C::NS * C::STAGE, "the output tile fits the stages");
   wait_vmcnt<0>();  // the copies of the steps past the end still land in their stages
   if constexpr (SPLIT) {
     // the slice's fp32 sums, 4 columns of one row per lane and register quad
@@ -753,6 +779,25 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, const GemmRegion&
     }
     return;
   }
+  store_tile<C, FP16>(p, rg, m0, n0, acc, lds, wave, lane);
+}
+
+// The tile's outputs: out[m][n..n+3] = round(acc * (sa * sw) + bias[n..n+3]),
+// staged through LDS (the stage memory, once every copy has landed): a
+// lane's results are 4 columns of one row, so stored straight from the
+// accumulators every store instruction would touch 32 rows; from LDS each one
+// writes whole rows of the tile (64 lanes x 16 B).  Staged row ml keeps its
+// 16-byte chunk c at physical chunk c ^ (ml % CPR), which spreads a
+// fragment's 32 rows over the banks.
+template <class C, bool FP16>
+__device__ __forceinline__ void store_tile(const GemmParams& p, const GemmRegion& rg, const int m0, const int n0,
+                                           const f32x16 (&acc)[C::NJ][C::MI], unsigned char* lds, const int wave,
+                                           const int lane) {
+  const int wm = wave % C::WGM, wn = wave / C::WGM;
+  constexpr int RB = C::BN * 2;   // bytes of a staged row
+  constexpr int CPR = RB / 16;    // 16-byte chunks per row
+  constexpr int RPI = 64 / CPR;   // rows per store instruction
+  static_assert(C::BM * RB <= C::NS * C::STAGE, "the output tile fits the stages");
   __syncthreads();  // and every wave is done with the last stage's fragments
   {
 #pragma clang fp contract(off)
@@ -797,6 +842,179 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, const GemmRegion&
   }
 }
 
+// One BM x BN output tile with 128 k-bytes per stage (CfgK128).  Layout of a
+// stage in LDS: A rows [BM][128 B], then W rows [BN][128 B]; the 16-byte chunk
+// c of row r sits at physical chunk c ^ swz8(r), swz8(r) = (r >> 1) & 7: a
+// fragment read (16 lanes on 16 consecutive rows, one chunk each) then
+// touches all 64 banks once, and a 1 KiB copy (8 rows x 8 chunks) writes one
+// contiguous KiB.  Each step of 128 k-bytes runs two MFMA k-steps:
+//   A: the MFMAs of the stage's first half, with the reads of its second half
+//      between the first half of them;
+//   then the wait for the next stage's copies and one barrier, which
+//   publishes the next stage and releases this one (every wave has read both
+//   of its halves; the barrier's LDS fence waits for those reads);
+//   B: the MFMAs of the second half, with the reads of the next stage's first
+//      half and the copies of the stage after next (into this stage's memory)
+//      spread between all of them.
+// Interleaved on one box against the 64-byte form (4 stages, a barrier per
+// MFMA k-step): 4352 x 9216 x 3072 103.8 against 110.0 us, 4352 x 12288 x 3072
+// 137.2 / 146.0, 4352 x 3072 x 12288 120.8 / 127.7, 4096 x 4096 x 12288
+// 137.1 / 151.1; with B's copies after its second half of MFMAs only (as the
+// 64-byte form places them) the gain was 0-5%, and spreading them in the
+// 64-byte form changed nothing.
+template <class C, bool FP16>
+__device__ __forceinline__ void gemm_tile_k128(const GemmParams& p, const GemmRegion& rg, const int bx,
+                                               unsigned char* lds) {
+  static_assert(C::KB == 128 && C::NS == 2, "two stages of 128 k-bytes");
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: copy targets go to SGPRs
+  const int wm = wave % C::WGM, wn = wave / C::WGM;
+
+  int m0, n0;
+  if (!tile_origin<C>(rg, bx, m0, n0)) return;
+  const int mrows = min(C::BM, p.M - m0);
+  const int nrows = min(C::BN, rg.N - n0);
+
+  // per-lane copy offsets: copy i of this wave fills 8-row group wave + NW i
+  // of its tile; lane l writes row l/8 of the group, physical chunk l%8, which
+  // holds logical chunk (l%8) ^ swz8(row).  NW is even, so the groups of one
+  // wave share swz8 and one chunk offset serves all of its copies.
+  const int crow = wave * 8 + (lane >> 3);
+  const int cchunk = ((lane & 7) ^ ((crow >> 1) & 7)) * 16;
+  uint32_t aoff[C::AI], woff[C::WI];
+#pragma unroll
+  for (int i = 0; i < C::AI; ++i) aoff[i] = (uint32_t)((crow + 8 * C::NW * i) * p.lda + cchunk);
+#pragma unroll
+  for (int i = 0; i < C::WI; ++i) woff[i] = (uint32_t)((crow + 8 * C::NW * i) * p.ldw + cchunk);
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_ptr_t)lds;
+  const unsigned char* abase = p.a + (int64_t)m0 * p.lda;
+  const unsigned char* wbase = rg.w + (int64_t)n0 * p.ldw;
+  const int nk = (p.K + C::KB - 1) / C::KB;
+
+  // copy state of one step, as in gemm_tile: past the end of K a lane's chunk
+  // gets the top offset bit (it lands as zeros), and a step at or past the
+  // end gets empty resources, so every step issues the same copies
+  struct StepCopies {
+    u32x4 ra, rw;
+    uint32_t st;
+    uint32_t dead;
+  };
+  auto prepare = [&](const int kt) __attribute__((always_inline)) {
+    StepCopies sc;
+    const int koff = kt * C::KB;
+    const int lim = p.K - koff;
+    const int kin = min(C::KB, lim);
+    sc.ra = rsrc_words(abase + koff, kt < nk ? (uint32_t)((mrows - 1) * p.lda + kin) : 0u);
+    sc.rw = rsrc_words(wbase + koff, kt < nk ? (uint32_t)((nrows - 1) * p.ldw + kin) : 0u);
+    sc.st = lds0 + (uint32_t)((kt & 1) * C::STAGE);
+    sc.dead = (lim < C::KB && cchunk >= lim) ? 0x80000000u : 0u;
+    return sc;
+  };
+  auto issue = [&](const StepCopies& sc, const int i) __attribute__((always_inline)) {
+    if (i < C::AI) dma16(sc.ra, sc.st + (uint32_t)((wave + C::NW * i) * 1024), aoff[i] | sc.dead);
+    else dma16(sc.rw, sc.st + (uint32_t)(C::A_BYTES + (wave + C::NW * (i - C::AI)) * 1024), woff[i - C::AI] | sc.dead);
+  };
+
+  // fragment reads: lane l reads row l%32 of a 32-row block, logical chunks
+  // 4h + 2(l/32) and 4h + 2(l/32) + 1 of k-half h; blocks start at multiples
+  // of 32 rows, so swz8 of the row is swz8(l%32)
+  const int frow = lane & 31;
+  uint32_t fo[2][2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int e = 0; e < 2; ++e)
+      fo[h][e] = (uint32_t)(frow * C::KB + ((4 * h + 2 * (lane >> 5) + e) ^ ((frow >> 1) & 7)) * 16);
+  constexpr int NRD = 2 * (C::MI + C::NJ);
+  // half r % 2 of fragment r / 2 (A fragments first, then W), k-half h of stage kt
+  auto read_frag = [&](const int kt, const int h, const int r, i32x8 (&fa)[C::MI], i32x8 (&fw)[C::NJ])
+      __attribute__((always_inline)) {
+    const unsigned char* st = lds + (kt & 1) * C::STAGE;
+    const int f = r >> 1;
+    const unsigned char* b = f < C::MI ? st + (wm * C::WM + f * 32) * C::KB
+                                       : st + C::A_BYTES + (wn * C::WN + (f - C::MI) * 32) * C::KB;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(b + fo[h][r & 1]);
+    i32x8& dst = f < C::MI ? fa[f] : fw[f - C::MI];
+    const int e = (r & 1) * 4;
+    dst[e] = (int)v.x;
+    dst[e + 1] = (int)v.y;
+    dst[e + 2] = (int)v.z;
+    dst[e + 3] = (int)v.w;
+  };
+
+  f32x16 acc[C::NJ][C::MI];
+#pragma unroll
+  for (int j = 0; j < C::NJ; ++j)
+#pragma unroll
+    for (int i = 0; i < C::MI; ++i) acc[j][i] = f32x16{};
+
+  // prologue: both stages in flight, stage 0 published, its first half read
+  {
+    const StepCopies s0 = prepare(0);
+#pragma unroll
+    for (int c = 0; c < C::COPIES; ++c) issue(s0, c);
+    const StepCopies s1 = prepare(1);
+#pragma unroll
+    for (int c = 0; c < C::COPIES; ++c) issue(s1, c);
+  }
+  wait_vmcnt<C::COPIES>();
+  __syncthreads();
+  i32x8 fa[2][C::MI], fw[2][C::NJ];
+#pragma unroll
+  for (int r = 0; r < NRD; ++r) read_frag(0, 0, r, fa[0], fw[0]);
+
+  // one MFMA k-step on fragments `cur`; reads of (stage rkt, half rh) into the
+  // other fragments after MFMAs [0, H); with COPY, the copies of sc after
+  // MFMAs [CB, NMF)
+  constexpr int NMF = C::NJ * C::MI;
+  auto kstep = [&](auto copy_tag, const int cur, const int rkt, const int rh, const StepCopies& sc)
+      __attribute__((always_inline)) {
+    constexpr bool COPY = decltype(copy_tag)::value;
+    constexpr int H = COPY ? NMF : (NMF >= 2 ? NMF / 2 : 1);
+    constexpr int CB = 0;
+    constexpr int CN = NMF - CB;
+#pragma unroll
+    for (int idx = 0; idx < NMF; ++idx) {
+      const int j = idx / C::MI, i = idx % C::MI;
+      acc[j][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fw[cur][j], fa[cur][i], acc[j][i], 0, 0, 0, 0,
+                                                                   0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      if (idx < H) {
+#pragma unroll
+        for (int r = idx * NRD / H; r < (idx + 1) * NRD / H; ++r) read_frag(rkt, rh, r, fa[cur ^ 1], fw[cur ^ 1]);
+      }
+      if constexpr (COPY) {
+        if (idx >= CB) {
+#pragma unroll
+          for (int c = (idx - CB) * C::COPIES / CN; c < (idx - CB + 1) * C::COPIES / CN; ++c) issue(sc, c);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  for (int kt = 0; kt < nk; ++kt) {
+    const StepCopies none = {};
+    kstep(std::false_type{}, 0, kt, 1, none);
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vmcnt<0>();  // the next stage's copies (issued one step ago) have landed
+    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+    const StepCopies sc = prepare(kt + 2);
+    kstep(std::true_type{}, 1, kt + 1, 0, sc);
+  }
+
+  wait_vmcnt<0>();  // the copies of the steps past the end still land in their stages
+  store_tile<C, FP16>(p, rg, m0, n0, acc, lds, wave, lane);
+}
+
+// A tile of either form.
+template <class C, bool FP16>
+__device__ __forceinline__ void run_tile(const GemmParams& p, const GemmRegion& rg, const int bx, unsigned char* lds) {
+  if constexpr (C::KB == 128) gemm_tile_k128<C, FP16>(p, rg, bx, lds);
+  else gemm_tile<C, FP16>(p, rg, bx, lds);
+}
+
 // Workgroups [0, r[0].wgs) compute region 0 with C1 tiles, the rest region 1
 // with C2 tiles.  The dispatcher starts workgroups in index order, so the
 // smaller tiles of region 1 fill the CUs that the last round of region 0
@@ -808,8 +1026,8 @@ fp8_gemm_kernel(const GemmParams p) {
   constexpr int LDS1 = C1::NS * C1::STAGE, LDS2 = C2::NS * C2::STAGE;
   __shared__ __attribute__((aligned(1024))) unsigned char lds[LDS1 > LDS2 ? LDS1 : LDS2];
   const int bx = blockIdx.x;
-  if (bx < p.r[0].wgs) gemm_tile<C1, FP16>(p, p.r[0], bx, lds);
-  else gemm_tile<C2, FP16>(p, p.r[1], bx - p.r[0].wgs, lds);
+  if (bx < p.r[0].wgs) run_tile<C1, FP16>(p, p.r[0], bx, lds);
+  else run_tile<C2, FP16>(p, p.r[1], bx - p.r[0].wgs, lds);
 }
 
 // Split launch: workgroup b sums k-slice b / wgs of tile b % wgs of region 0
@@ -995,12 +1213,14 @@ int launch_quant(const qik_fp8_quant_args* a, unsigned* ws, hipStream_t s) {
 }
 
 // GEMM tile shapes, largest first
-// The 256-row pair runs 8 waves, two per SIMD (2 x 4 waves, 128 x 64 wave
-// tiles, 128 accumulators and 236 registers per wave): interleaved on one
-// box against 4 waves of 128 x 128, 4352 x 9216 x 3072 109.4 against 113.1 us,
-// 4352 x 12288 x 3072 145.8 / 150.6, 4352 x 3072 x 12288 128.7 / 129.3.
-typedef Cfg<256, 256, 4, 2, 4> Cfg256x256;
-typedef Cfg<256, 128, 4, 2, 4> Cfg256x128w8;
+// The 256-row pair: 128 k-bytes per stage (CfgK128) and 8 waves, two per
+// SIMD (2 x 4 waves, 128 x 64 wave tiles, 128 accumulators and 240 registers
+// per wave).  With 64 k-bytes per stage, 8 waves against 4 of 128 x 128:
+// 4352 x 9216 x 3072 109.4 against 113.1 us, 4352 x 12288 x 3072 145.8 /
+// 150.6, 4352 x 3072 x 12288 128.7 / 129.3 (interleaved on one box); with 128,
+// 4 waves were within 2% of 8 either way.
+typedef CfgK128<256, 256, 2, 4> Cfg256x256;
+typedef CfgK128<256, 128, 2, 4> Cfg256x128w8;
 typedef Cfg<256, 128, 4> Cfg256x128;
 // The smaller tiles' k-steps are short (four and one MFMAs per wave), so they
 // keep more stages in flight to cover the copies' latency: at 256 x 3072 x

@@ -202,14 +202,15 @@ def _half_ulp(v, dtype):
 
 def _check_close(out, ref, abs_sum):
     """out = round(y) with y the kernel's fp32 result; ref the fp64 value.
-    |y - ref| <= acc := 2^-16 * sum_k |A[m,k] W[n,k]| * scales + |bias|: the
+    |y - ref| <= acc := 2^-14 * sum_k |A[m,k] W[n,k]| * scales + |bias|: the
     fp8 matrix cores sum each block of 64 products in their own way (not an
     IEEE fp32 loop: the kernel matches hipBLASLt's fp8 GEMM bit for bit, not a
-    sequential fp32 sum; the largest error seen is about 2^-18 of the sum),
+    sequential fp32 sum; the largest error seen is about 2^-15 of the sum, at
+    one element of 4352 x 3072 x 80, where hipBLASLt gives the same bits),
     then the fp32 accumulation, scale and bias steps.  So |out - ref| <= half an
     output ulp at |ref| + acc, + acc."""
     o = out.double().cpu().numpy()
-    acc = 2.0 ** -16 * abs_sum
+    acc = 2.0 ** -14 * abs_sum
     bound = _half_ulp(np.abs(ref) + acc, out.dtype) + 2 * acc
     err = np.abs(o - ref)
     bad = err > bound
@@ -242,6 +243,9 @@ def _abs_sum(xq, wq, sx, sw, bias):
     (1543, 9232, 1104),   # 256 x 256 tiles on columns [0, 8192), 256 x 128 on the rest
     (803, 8416, 1104),    # 256 x 128 tiles on columns [0, 6400), 128 x 128 on the rest
     (256, 1552, 3072),    # 128 x 128 or 64 x 64 tiles, ragged N
+    (4352, 3072, 80),     # 256 x 256 tiles (128 k-bytes per stage): one stage, 80 of its bytes
+    (2304, 2560, 144),    # two stages, the second 16 bytes deep
+    (2000, 4400, 400),    # ragged M and N, 256 x 256 then 256 x 128 columns, a 16-byte k tail
 ])
 @pytest.mark.parametrize("bias", [False, True])
 def test_gemm_vs_fp64_oracle(qik, M, N, K, bias):
@@ -429,7 +433,8 @@ def test_convert_linears_fp8_and_state_dict(qik):
 @pytest.mark.parametrize("M,N,K,bias", [(1536, 4096, 4096, False), (4352, 3072, 3072, True),
                                         (300, 272, 4096, True), (513, 1040, 1104, False),
                                         (4352, 9216, 3072, True), (803, 8416, 1104, True),
-                                        (256, 3072, 12288, True)])
+                                        (256, 3072, 12288, True), (4352, 3072, 80, False),
+                                        (2000, 4400, 400, True)])
 def test_gemm_matches_torch_scaled_mm(qik, M, N, K, bias):
     """torch._scaled_mm is the call the reference makes (fp8.py:87-88); on this
     device it is hipBLASLt's fp8 GEMM.  The kernel agrees with it on (almost)
