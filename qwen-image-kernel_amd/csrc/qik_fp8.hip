@@ -1228,7 +1228,13 @@ typedef Cfg<256, 128, 4> Cfg256x128;
 // at 256 x 9216 x 3072 (128 x 128) 6 stages 17.0 against 18.8 with 4.
 typedef Cfg<128, 128, 6> Cfg128x128;
 typedef Cfg<64, 64, 8> Cfg64x64;
-typedef Cfg<192, 128, 4> Cfg192x128;
+// The 192-row pair (the reference test's 1536 x 4096 x 4096 takes 256 of its
+// tiles) at 128 k-bytes per stage, 4 waves: 1536 x 4096 x 4096 30.2-31.9
+// against 31.2-33.8 us, 1536 x 4096 x 12288 82.4 / 86.0, interleaved on one
+// box.  The 256 x 128 / 128 x 128 pair stays at 64 k-bytes: at 128 (4 waves,
+// eight MFMAs per step) 768 x 3072 x 12288 took 67.7 against 54.4 us.
+typedef CfgK128<192, 128, 2, 2> Cfg192x128k;
+typedef CfgK128<128, 128, 2, 2> Cfg128x128k;
 
 // Time of a tile of each shape relative to a 256 x 256 tile: area / rate,
 // the rates measured on MI355X with each shape forced over whole launches
@@ -1559,7 +1565,7 @@ int qik_fp8_gemm(const qik_fp8_gemm_args* a, void* stream) {
   switch (plan.pair) {
     case 0: return launch_gemm<Cfg256x256, Cfg256x128w8>(p, a, plan.n1, fp16, s);
     case 1: return launch_gemm<Cfg256x128, Cfg128x128>(p, a, plan.n1, fp16, s);
-    case 2: return launch_gemm<Cfg192x128, Cfg128x128>(p, a, plan.n1, fp16, s);
+    case 2: return launch_gemm<Cfg192x128k, Cfg128x128k>(p, a, plan.n1, fp16, s);
     default: return launch_gemm<Cfg128x128, Cfg64x64>(p, a, plan.n1, fp16, s);
   }
 }
