@@ -518,6 +518,28 @@ def test_benchmark_shapes_all_heads_vs_torch_fp32(name):
     assert d.max().item() <= MAX_ABS and d.mean().item() <= MEAN_ABS, (d.max().item(), d.mean().item())
 
 
+def test_multiref_all_heads_vs_host_explicit_mask_sdpa():
+    """Every (b, h) of multiref_cfg (48) against the fp32 explicit-mask SDPA on
+    the host (oracle.attention.CpuSdpaBaseline, which the oracle tests pin to
+    attention_fp32), at the parity bar."""
+    _flush("case multiref_cfg all 48 (b, h) vs host")
+    wl = wls.workload("multiref_cfg")
+    inp = wls.make_inputs(wl, seed=5000, device=DEV)
+    out = _wl_run(wl, inp).float().cpu()
+    cpu = {k: (v.cpu() if isinstance(v, torch.Tensor) else v) for k, v in inp.items()}
+    base = oa.CpuSdpaBaseline(cpu["query"], cpu["key"], cpu["value"], wl.lengths(), cpu["cache_k"],
+                              cpu["cache_v"], cpu["cache_v_scale"])
+    mx, total, n = 0.0, 0.0, 0
+    for b in range(wl.B):
+        for h in range(wl.H):
+            d = (out[b, :, h] - base.run(b, h)).abs()
+            mx = max(mx, d.max().item())
+            total += d.sum().item()
+            n += d.numel()
+    _flush(f"  multiref_cfg all heads: max {mx:.2e} mean {total / n:.2e}")
+    assert mx <= MAX_ABS and total / n <= MEAN_ABS, (mx, total / n)
+
+
 @pytest.mark.parametrize("name,H", [("t2i_1024", 25), ("edit_768", 25), ("multiref_cfg", 13)])
 def test_odd_head_counts_all_heads_vs_torch_fp32(name, H):
     """Head counts whose row blocks do not split evenly over the 8 XCDs (the
