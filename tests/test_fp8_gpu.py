@@ -246,6 +246,7 @@ def _abs_sum(xq, wq, sx, sw, bias):
     (4352, 3072, 80),     # 256 x 256 tiles (128 k-bytes per stage): one stage, 80 of its bytes
     (2304, 2560, 144),    # two stages, the second 16 bytes deep
     (2000, 4400, 400),    # ragged M and N, 256 x 256 then 256 x 128 columns, a 16-byte k tail
+    (2000, 4400, 12304),  # the same with a long K: 96 stages of 128 bytes and a 16-byte tail
 ])
 @pytest.mark.parametrize("bias", [False, True])
 def test_gemm_vs_fp64_oracle(qik, M, N, K, bias):
