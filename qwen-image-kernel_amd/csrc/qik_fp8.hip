@@ -4,23 +4,28 @@
 // replaces torch._scaled_mm (fp8.py:87-88), and the weight dequantisation of
 // the bf16 path for layers with fewer than 256 inputs (fp8.py:79-84).
 //
-// The quantiser is an HBM-bound two-pass byte mover (max |x| per block into a
-// small workspace, then every block re-reduces those maxima, forms the scale
-// and writes the codes).  Contraction is off in it, so every fp32 multiply
-// and division rounds on its own, as torch's elementwise ops do.
+// The quantiser is an HBM-bound byte mover: when the tensor fits the
+// registers of the resident workgroups, one launch in which every workgroup
+// holds its share, publishes its max |x| and reads everyone else's before it
+// writes its codes; otherwise two passes (max |x| per block into a small
+// workspace, then every block re-reduces those maxima, forms the scale and
+// writes the codes).  Contraction is off in it, so every fp32 multiply and
+// division rounds on its own, as torch's elementwise ops do.  Weights in host
+// memory are quantised on the host with torch's CPU rounding.
 //
 // The GEMM runs on the gfx950 fp8 matrix cores: v_mfma_f32_32x32x64_f8f6f4
 // (e4m3 x e4m3, fp32 accumulate; 32x32 outputs x 64 k per instruction, twice
-// the k of the CDNA3 fp8 MFMA).  One workgroup of 4 waves computes a BM x BN
-// tile of out^T = W . A^T (MFMA A operand = weight rows n, B operand =
-// activation rows m), so each lane ends with 4 consecutive n of one row m per
-// register quad and stores 8 contiguous bytes.  Tiles of A and W, 64 k-bytes
-// per stage, reach LDS directly (buffer_load_dwordx4 ... lds, no register
-// staging) NS-1 stages ahead of their use, with a 16-byte chunk swizzle that
-// makes the fragment reads conflict-free; each wave reads the next stage's
-// fragments while its MFMAs run on the current one, and the copies are issued
-// between the MFMAs.  Workgroups map to tiles XCD by XCD (the dispatcher deals
-// workgroup b to XCD b % 8), so one XCD's L2 serves a compact block of tiles.
+// the k of the CDNA3 fp8 MFMA).  One workgroup of 4 or 8 waves computes a
+// BM x BN tile of out^T = W . A^T (MFMA A operand = weight rows n, B operand
+// = activation rows m), so each lane ends with 4 consecutive n of one row m
+// per register quad.  Tiles of A and W reach LDS directly
+// (buffer_load_dwordx4 ... lds, no register staging), 64 or 128 k-bytes per
+// stage, ahead of their use, with a 16-byte chunk swizzle that makes the
+// fragment reads conflict-free; each wave reads the next fragments while its
+// MFMAs run on the current ones, and the copies are issued between the MFMAs.
+// The outputs go out through LDS as whole rows.  Workgroups map to tiles XCD
+// by XCD (the dispatcher deals workgroup b to XCD b % 8), so one XCD's L2
+// serves a compact block of tiles.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
