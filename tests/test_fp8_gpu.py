@@ -454,3 +454,37 @@ def test_gemm_matches_torch_scaled_mm(qik, M, N, K, bias):
     d = (got.double() - want.double()).abs()
     step = torch.from_numpy(2 * _half_ulp(want.double().cpu().numpy(), torch.bfloat16)).to(DEV)
     assert (d <= step).all()
+
+
+def _random_gemm_shapes(n, seed):
+    """Seeded shapes over every tile plan: M from 1 to 5000, N and K multiples
+    of 16 up to 13000 and 6000 (ragged against every tile shape and both stage
+    depths)."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        M = int(rng.choice([rng.integers(1, 300), rng.integers(300, 2000), rng.integers(2000, 5000)]))
+        N = 16 * int(rng.integers(1, 13000 // 16))
+        K = 16 * int(rng.integers(1, 6000 // 16))
+        out.append((M, N, K))
+    return out
+
+
+@pytest.mark.parametrize("M,N,K", _random_gemm_shapes(14, 2024))
+def test_gemm_random_shapes_match_torch_scaled_mm(qik, M, N, K):
+    """Random shapes, through the entry point FP8Linear uses (qik_fp8_gemm_ws,
+    K split included): at least 99% of the outputs bit-identical to
+    torch._scaled_mm, the rest within one bf16 step."""
+    a, w, xq, wq, sx, sw = _gemm_operands(M, N, K, 7 * M + 3 * N + K)
+    sa, sb = torch.tensor([sx], device=DEV), torch.tensor([sw], device=DEV)
+    try:
+        want = torch._scaled_mm(a, w.t(), scale_a=sa, scale_b=sb, out_dtype=torch.bfloat16)
+    except (RuntimeError, NotImplementedError) as e:
+        pytest.skip(f"torch._scaled_mm unavailable here: {e}")
+    got = qik.fp8_linear(a, w, sa, sb, None)
+    same = (got.view(torch.int16) == want.view(torch.int16)).float().mean().item()
+    print(f"M={M} N={N} K={K}: {same:.6f} of the outputs bit-identical to torch._scaled_mm")
+    assert same >= 0.99
+    d = (got.double() - want.double()).abs()
+    step = torch.from_numpy(2 * _half_ulp(want.double().cpu().numpy(), torch.bfloat16)).to(DEV)
+    assert (d <= step).all()
