@@ -855,18 +855,20 @@ __device__ __forceinline__ void store_tile(const GemmParams& p, const GemmRegion
 // contiguous KiB.  Each step of 128 k-bytes runs two MFMA k-steps:
 //   A: the MFMAs of the stage's first half, with the reads of its second half
 //      between the first half of them;
-//   then the wait for the next stage's copies and one barrier, which
-//   publishes the next stage and releases this one (every wave has read both
-//   of its halves; the barrier's LDS fence waits for those reads);
-//   B: the MFMAs of the second half, with the reads of the next stage's first
-//      half and the copies of the stage after next (into this stage's memory)
-//      spread between all of them.
+//   B: the MFMAs of the second half: the first two, then the wait for the
+//      next stage's copies and one barrier, which publishes the next stage
+//      and releases this one (every wave has read both of its halves; the
+//      barrier's LDS fence waits for those reads), then the rest, with the
+//      reads of the next stage's first half and the copies of the stage after
+//      next (into this stage's memory) spread between them.
 // Interleaved on one box against the 64-byte form (4 stages, a barrier per
 // MFMA k-step): 4352 x 9216 x 3072 103.8 against 110.0 us, 4352 x 12288 x 3072
 // 137.2 / 146.0, 4352 x 3072 x 12288 120.8 / 127.7, 4096 x 4096 x 12288
 // 137.1 / 151.1; with B's copies after its second half of MFMAs only (as the
 // 64-byte form places them) the gain was 0-5%, and spreading them in the
-// 64-byte form changed nothing.
+// 64-byte form changed nothing.  Two of B's MFMAs ahead of the barrier: 0.7-5%
+// faster again (1536 x 4096 x 12288 77.5 against 81.5 us, 4352 x 3072 x 12288
+// 119.8 / 121.8), one or four: no better.
 template <class C, bool FP16>
 __device__ __forceinline__ void gemm_tile_k128(const GemmParams& p, const GemmRegion& rg, const int bx,
                                                unsigned char* lds) {
@@ -969,30 +971,39 @@ __device__ __forceinline__ void gemm_tile_k128(const GemmParams& p, const GemmRe
 #pragma unroll
   for (int r = 0; r < NRD; ++r) read_frag(0, 0, r, fa[0], fw[0]);
 
-  // one MFMA k-step on fragments `cur`; reads of (stage rkt, half rh) into the
-  // other fragments after MFMAs [0, H); with COPY, the copies of sc after
-  // MFMAs [CB, NMF)
+  // One MFMA k-step on fragments `cur`, with the reads of (stage rkt, half rh)
+  // into the other fragments between its MFMAs.  The second k-step (COPY)
+  // issues its first PRE MFMAs (their fragments are in registers) before the
+  // wait for the next stage's copies and the barrier, so the matrix core has
+  // work while the wave waits there; its reads and the copies of sc follow,
+  // spread over the remaining MFMAs.
   constexpr int NMF = C::NJ * C::MI;
+  constexpr int PRE = 2 < NMF ? 2 : NMF - 1;
   auto kstep = [&](auto copy_tag, const int cur, const int rkt, const int rh, const StepCopies& sc)
       __attribute__((always_inline)) {
     constexpr bool COPY = decltype(copy_tag)::value;
-    constexpr int H = COPY ? NMF : (NMF >= 2 ? NMF / 2 : 1);
-    constexpr int CB = 0;
-    constexpr int CN = NMF - CB;
+    constexpr int R0 = COPY ? PRE : 0;  // reads (and copies) after MFMAs [R0, R0 + H)
+    constexpr int H = COPY ? NMF - PRE : (NMF >= 2 ? NMF / 2 : 1);
 #pragma unroll
     for (int idx = 0; idx < NMF; ++idx) {
       const int j = idx / C::MI, i = idx % C::MI;
       acc[j][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fw[cur][j], fa[cur][i], acc[j][i], 0, 0, 0, 0,
                                                                    0, 0);
       __builtin_amdgcn_sched_barrier(0);
-      if (idx < H) {
-#pragma unroll
-        for (int r = idx * NRD / H; r < (idx + 1) * NRD / H; ++r) read_frag(rkt, rh, r, fa[cur ^ 1], fw[cur ^ 1]);
-      }
       if constexpr (COPY) {
-        if (idx >= CB) {
+        if (idx == PRE - 1) {
+          wait_vmcnt<0>();  // the next stage's copies (issued one step ago) have landed
+          __syncthreads();
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+      if (idx >= R0 && idx < R0 + H) {
 #pragma unroll
-          for (int c = (idx - CB) * C::COPIES / CN; c < (idx - CB + 1) * C::COPIES / CN; ++c) issue(sc, c);
+        for (int r = (idx - R0) * NRD / H; r < (idx - R0 + 1) * NRD / H; ++r)
+          read_frag(rkt, rh, r, fa[cur ^ 1], fw[cur ^ 1]);
+        if constexpr (COPY) {
+#pragma unroll
+          for (int c = (idx - R0) * C::COPIES / H; c < (idx - R0 + 1) * C::COPIES / H; ++c) issue(sc, c);
         }
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -1001,9 +1012,6 @@ __device__ __forceinline__ void gemm_tile_k128(const GemmParams& p, const GemmRe
   for (int kt = 0; kt < nk; ++kt) {
     const StepCopies none = {};
     kstep(std::false_type{}, 0, kt, 1, none);
-    __builtin_amdgcn_sched_barrier(0);
-    wait_vmcnt<0>();  // the next stage's copies (issued one step ago) have landed
-    __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
     const StepCopies sc = prepare(kt + 2);
     kstep(std::true_type{}, 1, kt + 1, 0, sc);
