@@ -405,7 +405,9 @@ __global__ void __launch_bounds__(NTHREADS * KSPLIT, (KSPLIT == 1 && D <= 128) ?
   // counter at the start of the launch queued behind each other); later
   // positions come from the counter, drawn at the end of a unit's tile loop so
   // that the atomic's round trip overlaps the unit's merge and store.
-  const bool pulled = args.ctl != nullptr;
+  // (the two-group kernel runs one unit per workgroup; a workspace there holds
+  // only the merge of split row blocks)
+  const bool pulled = KSPLIT == 1 && args.ctl != nullptr;
   const int nx = args.plan.nx;
   const int xcd = (int)(blockIdx.x % nx);
   const int gx = (int)(gridDim.x / nx);
@@ -436,10 +438,10 @@ __global__ void __launch_bounds__(NTHREADS * KSPLIT, (KSPLIT == 1 && D <= 128) ?
     const Params p = reread_args();
     Work wk = plan_work(p.plan, bidv);
     if (wk.item < 0) continue;
-    if constexpr (KSPLIT == 2) {
-      wk.piece = grp;  // the groups are the row block's two pieces
-      wk.group = 0;
-    }
+    // the lead thread of the workgroup (of group 0 in the two-group kernel,
+    // whose groups split the unit's tiles between them: wk.piece is the
+    // workgroup's piece of a row block split over two workgroups)
+    const bool lead = tid == 0 && grp == 0;
     const int vid = wk.item;
     const int nmb = p.plan.nmb;
     const int bh = vid / nmb;
@@ -553,7 +555,7 @@ __global__ void __launch_bounds__(NTHREADS * KSPLIT, (KSPLIT == 1 && D <= 128) ?
     // first tile with a cache, else the fresh keys' first): its copies go out
     // before the lengths are reduced.  With uniform lengths every unit's
     // tiles are known here.
-    const bool early = p.uniform || wk.piece == 0;
+    const bool early = p.uniform || (wk.piece == 0 && grp == 0);
     int run0 = 0, run1 = 0;
     auto schedule = [&]() {
       // KV-tile schedule: tile t of a segment starting at absolute key s0 is
@@ -561,18 +563,30 @@ __global__ void __launch_bounds__(NTHREADS * KSPLIT, (KSPLIT == 1 && D <= 128) ?
       run0 = (p.has_cache && Lmax >= 0) ? min(cdiv_i(p.P, BN), Lmax / BN + 1) : 0;
       run1 = (Lmax >= s1) ? min(cdiv_i(p.SN, BN), (Lmax - s1) / BN + 1) : 0;
     };
+    bool gsplit_on = false;  // two-group kernel: the unit's tiles are split between the groups
     auto piece_tiles = [&](int T, int& g0, int& g1) {
       // this unit's tiles [g0, g1): all of them, or one of the item's two
-      // pieces (T, and so the split, is the same for both pieces of the item);
-      // a second group with nothing to do gets an empty range
+      // pieces (T, and so the split, is the same for both pieces of the item)
       const bool split = wk.group >= 0 && T >= SPLIT_MIN_TILES;
-      // two-group kernel: group 0's waves are the older ones on every SIMD and
-      // win issue arbitration (measured: 9 tiles in 13.4 us against group 1's
-      // 17.0 us), so group 0 takes 9/16 of the tiles
-      const int gsplit = KSPLIT == 2 ? (9 * T + 8) / 16 : p.plan.even ? (T + 1) / 2 : (7 * T + 5) / 10;
-      g0 = (split && wk.piece) ? gsplit : 0;
-      g1 = (split && !wk.piece) ? gsplit : T;
-      if (KSPLIT == 2 && !split && wk.piece) g0 = T;
+      if constexpr (KSPLIT == 1) {
+        const int gsplit = p.plan.even ? (T + 1) / 2 : (7 * T + 5) / 10;
+        g0 = (split && wk.piece) ? gsplit : 0;
+        g1 = (split && !wk.piece) ? gsplit : T;
+      } else {
+        // the workgroup's part of the row block (all of it, or one of two equal
+        // halves), split between the groups; group 0's waves are the older ones
+        // on every SIMD and win issue arbitration (measured: 9 tiles in 13.4 us
+        // against group 1's 17.0 us), so group 0 takes 9/16 of the tiles, and a
+        // second group with nothing to do gets an empty range
+        const int h = (T + 1) / 2;
+        const int a = (split && wk.piece) ? h : 0;
+        const int e = (split && !wk.piece) ? h : T;
+        gsplit_on = e - a >= SPLIT_MIN_TILES;
+        const int mid = a + (9 * (e - a) + 8) / 16;
+        g0 = (gsplit_on && grp) ? mid : a;
+        g1 = (gsplit_on && !grp) ? mid : e;
+        if (!gsplit_on && grp) g0 = e;
+      }
       return split;
     };
     if (p.uniform) {
@@ -584,7 +598,7 @@ __global__ void __launch_bounds__(NTHREADS * KSPLIT, (KSPLIT == 1 && D <= 128) ?
         issue_seg(seg0, seg0 ? e0 : e0 - run0, 0);
       }
     } else {
-      if (wk.piece == 0) issue_seg(p.has_cache != 0, 0, 0);
+      if (early) issue_seg(p.has_cache != 0, 0, 0);
       Lrow = live ? Lraw : -1;
       const int lmax = wave_reduce_i32<true>(live ? Lrow : -1);
       wave_minL = wave_reduce_i32<false>(live ? Lrow : INT_MAX);
@@ -599,11 +613,11 @@ __global__ void __launch_bounds__(NTHREADS * KSPLIT, (KSPLIT == 1 && D <= 128) ?
     }
     const int T = run0 + run1;
 
-    if (p.debug_tiles != nullptr && tid == 0 && wk.piece == 0) p.debug_tiles[bh * nmb + mb] = T;
+    if (p.debug_tiles != nullptr && lead && wk.piece == 0) p.debug_tiles[bh * nmb + mb] = T;
 
     int g0, g1;
     const bool split = piece_tiles(T, g0, g1);
-    if (KSPLIT == 1 && wk.piece > 0 && !split) continue;
+    if (wk.piece > 0 && !split) continue;
 
     // ---- LDS operand offsets inside a stage (lane constants)
     const int swk = swz<CH>(l32);  // rows l32 and l32 + 32 share it
@@ -815,9 +829,8 @@ __global__ void __launch_bounds__(NTHREADS * KSPLIT, (KSPLIT == 1 && D <= 128) ?
     const Params pe = reread_args();
     if (pulled && tid == 0) pend = g_fetch_add(pe.ctl + xcd, 1u);
     drawn = pulled;
-    float l_part = l_run;
     if constexpr (KSPLIT == 2) {
-      if (split) {
+      if (gsplit_on) {
         // group 1 hands its O^T accumulators and (m, l) to group 0 through
         // its own stage block (free: the tile loop ended with a barrier), and
         // group 0 combines the two in piece order, the arithmetic of the
@@ -840,7 +853,8 @@ __global__ void __launch_bounds__(NTHREADS * KSPLIT, (KSPLIT == 1 && D <= 128) ?
           const float mm = fmaxf(m0, m1);
           const float a0 = (m0 == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m0 - mm);
           const float a1 = (m1 == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m1 - mm);
-          l_part = l_run * a0 + mlo[1] * a1;
+          l_run = l_run * a0 + mlo[1] * a1;
+          m_run = mm;
 #pragma unroll
           for (int db = 0; db < DBLK; ++db)
 #pragma unroll
@@ -851,7 +865,12 @@ __global__ void __launch_bounds__(NTHREADS * KSPLIT, (KSPLIT == 1 && D <= 128) ?
             }
         }
       }
-    } else if (split) {
+      // a timed-out group barrier poisons the row sums (before any merge
+      // through the workspace, which carries them on)
+      if (!synced) l_run = __builtin_nanf("");
+    }
+    float l_part = l_run;
+    if (split) {
       constexpr int OB = slot_oacc_bytes<D>();
       constexpr int SB = slot_bytes<D>();
       constexpr int SC1 = 16;  // cache policy: device scope
@@ -861,27 +880,29 @@ __global__ void __launch_bounds__(NTHREADS * KSPLIT, (KSPLIT == 1 && D <= 128) ?
       // it back).  A piece that finds the other one already arrived merges
       // at once and never writes its own slot; otherwise it publishes its
       // slot and arrives, and the second to arrive merges.
-      if (tid == 0) sred[0][0] = g_load(word) == 1u ? 1 : 0;
+      if (lead) sred[0][0] = g_load(word) == 1u ? 1 : 0;
       __syncthreads();
       const bool other_first = sred[0][0] != 0;
       __syncthreads();  // every thread has read the flag before it is reused
       if (other_first) {
-        if (tid == 0) g_store(word, 0u);
+        if (lead) g_store(word, 0u);
       } else {
         const auto mine = make_rsrc(gslots + wk.piece * SB, SB);
+        if (grp == 0) {
 #pragma unroll
-        for (int db = 0; db < DBLK; ++db)
+          for (int db = 0; db < DBLK; ++db)
 #pragma unroll
-          for (int q4 = 0; q4 < 4; ++q4) {
-            const f32x4 v = {oacc[db][4 * q4 + 0], oacc[db][4 * q4 + 1], oacc[db][4 * q4 + 2], oacc[db][4 * q4 + 3]};
-            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), mine,
-                                                   (uint32_t)(((db * 4 + q4) * NTHREADS + tid) * 16), 0, SC1);
-          }
-        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f32x2{m_run, l_run}), mine,
-                                              (uint32_t)(OB + tid * 8), 0, SC1);
+            for (int q4 = 0; q4 < 4; ++q4) {
+              const f32x4 v = {oacc[db][4 * q4 + 0], oacc[db][4 * q4 + 1], oacc[db][4 * q4 + 2], oacc[db][4 * q4 + 3]};
+              __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), mine,
+                                                     (uint32_t)(((db * 4 + q4) * NTHREADS + tid) * 16), 0, SC1);
+            }
+          __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f32x2{m_run, l_run}), mine,
+                                                (uint32_t)(OB + tid * 8), 0, SC1);
+        }
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the slot has reached device scope
         __syncthreads();
-        if (tid == 0) {
+        if (lead) {
           const unsigned before = g_fetch_add(word, 1u);
           const bool last = before == 1u;
           if (last) g_store(word, 0u);
@@ -893,30 +914,33 @@ __global__ void __launch_bounds__(NTHREADS * KSPLIT, (KSPLIT == 1 && D <= 128) ?
       }
 
       // the other piece's state; the two combine in piece order, the same
-      // arithmetic whichever of them arrived last
-      const auto other = make_rsrc(gslots + (wk.piece ^ 1) * SB, SB);
-      const f32x2 mlo = __builtin_bit_cast(
-          f32x2, __builtin_amdgcn_raw_buffer_load_b64(other, (uint32_t)(OB + tid * 8), 0, SC1));
-      const bool p1 = wk.piece != 0;
-      const float m0 = p1 ? mlo[0] : m_run, m1 = p1 ? m_run : mlo[0];
-      const float l0 = p1 ? mlo[1] : l_run, l1 = p1 ? l_run : mlo[1];
-      const float mm = fmaxf(m0, m1);
-      const float a0 = (m0 == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m0 - mm);
-      const float a1 = (m1 == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m1 - mm);
-      l_part = l0 * a0 + l1 * a1;
+      // arithmetic whichever of them arrived last (in the two-group kernel
+      // group 0 holds the workgroup's state and stores the rows)
+      if (KSPLIT == 1 || grp == 0) {
+        const auto other = make_rsrc(gslots + (wk.piece ^ 1) * SB, SB);
+        const f32x2 mlo = __builtin_bit_cast(
+            f32x2, __builtin_amdgcn_raw_buffer_load_b64(other, (uint32_t)(OB + tid * 8), 0, SC1));
+        const bool p1 = wk.piece != 0;
+        const float m0 = p1 ? mlo[0] : m_run, m1 = p1 ? m_run : mlo[0];
+        const float l0 = p1 ? mlo[1] : l_run, l1 = p1 ? l_run : mlo[1];
+        const float mm = fmaxf(m0, m1);
+        const float a0 = (m0 == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m0 - mm);
+        const float a1 = (m1 == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m1 - mm);
+        l_part = l0 * a0 + l1 * a1;
 #pragma unroll
-      for (int db = 0; db < DBLK; ++db)
+        for (int db = 0; db < DBLK; ++db)
 #pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-          const f32x4 v = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                        other, (uint32_t)(((db * 4 + q4) * NTHREADS + tid) * 16), 0, SC1));
+          for (int q4 = 0; q4 < 4; ++q4) {
+            const f32x4 v = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                          other, (uint32_t)(((db * 4 + q4) * NTHREADS + tid) * 16), 0, SC1));
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float o0 = p1 ? v[e] : oacc[db][4 * q4 + e];
-            const float o1 = p1 ? oacc[db][4 * q4 + e] : v[e];
-            oacc[db][4 * q4 + e] = o0 * a0 + o1 * a1;
+            for (int e = 0; e < 4; ++e) {
+              const float o0 = p1 ? v[e] : oacc[db][4 * q4 + e];
+              const float o1 = p1 ? oacc[db][4 * q4 + e] : v[e];
+              oacc[db][4 * q4 + e] = o0 * a0 + o1 * a1;
+            }
           }
-        }
+      }
     }
 
     // ---- epilogue: out = l > 0 ? acc / l : 0 (triton_attention.py:166-168).
@@ -1193,11 +1217,25 @@ int plan_launch(const qik_attn_args* a, bool split, Launch* L) {
   if (n == 0) return QIK_OK;
   const int nx = device_xcds();
   int sx = 1;
-  if (split && two_group_dim(a->D) && n <= device_cus()) {
+  const int cus = device_cus();
+  if (split && two_group_dim(a->D) && n <= cus) {
     // row blocks fit the CUs once: one two-group workgroup per row block, its
-    // KV tiles split between the groups and merged in LDS (no workspace)
+    // KV tiles split between the groups and merged in LDS (no workspace) ...
     L->fn = pick_kernel_d(a->D, fp16, vfp8, kv, true);
     L->threads = 2 * NTHREADS;
+    if (2 * n <= cus && cus >= nx) {
+      // ... or, with at most half the CUs' worth of row blocks (one GPU's share
+      // of the heads), each row block split into two equal pieces on two CUs,
+      // every piece split between the groups, the pieces merged through the
+      // workspace as the split launch below merges them
+      L->plan = make_plan((int)n, (int)nmb, cus / nx, 1, (a->flags & QIK_UNIFORM_L) ? 0 : 1, nx);
+      if (L->plan.ns == 2 && L->plan.wpx <= cus / nx && 2 * NXCD_MAX + L->plan.ngroups <= QIK_ATTN_WS_CTL_BYTES / 4) {
+        L->grid = (int64_t)nx * L->plan.wpx;
+        L->ctl_bytes = QIK_ATTN_WS_CTL_BYTES;
+        L->ws_bytes = L->ctl_bytes + (int64_t)L->plan.ngroups * L->plan.ns * L->slot;
+        return QIK_OK;
+      }
+    }
     L->plan = make_plan((int)n, (int)nmb, 1, 0, 1, nx);
     L->grid = (int64_t)nx * L->plan.wpx;
     return QIK_OK;

@@ -555,6 +555,22 @@ def test_odd_head_counts_all_heads_vs_torch_fp32(name, H):
     assert d.max().item() <= MAX_ABS and d.mean().item() <= MEAN_ABS, (d.max().item(), d.mean().item())
 
 
+@pytest.mark.parametrize("name,H", [("t2i_1024", 3), ("edit_768", 3), ("t2i_512", 3), ("multiref_cfg", 1),
+                                    ("t2i_1024", 1), ("edit_768", 5)])
+def test_one_gpu_head_share_all_heads_vs_torch_fp32(name, H):
+    """One GPU's share of the heads (H/8 of 24 at the 1024px and 768px shapes:
+    the two-group launch with every row block split over two CUs and merged
+    through the workspace) against the torch fp32 reference."""
+    _flush(f"case head share {name} H={H}")
+    wl = dataclasses.replace(wls.workload(name), H=H)
+    inp = wls.make_inputs(wl, seed=93, device=DEV, gen_device="cuda")
+    out = _wl_run(wl, inp).float()
+    ref = _torch_fp32_reference(wl, inp)
+    d = (out - ref).abs()
+    assert torch.isfinite(out).all()
+    assert d.max().item() <= MAX_ABS and d.mean().item() <= MEAN_ABS, (d.max().item(), d.mean().item())
+
+
 def test_layers_independent_seeds_size_independent_property():
     """Linearity in V at full 1024px size: attn(q,k,a*v1+b*v2) ~= a*attn(q,k,v1)+b*attn(q,k,v2)."""
     wl = wls.workload("t2i_1024")

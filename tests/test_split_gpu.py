@@ -1,12 +1,15 @@
 """GPU parity of the split launches of qik_attn_fwd_ws.
 
-Two forms, chosen by the number of row blocks n:
+Three forms, chosen by the number of row blocks n:
 * n above the CU count: each row block of the launch's last, partly filled
   round runs as two pieces over its KV tiles, which meet in a workspace, and
   the launch's resident workgroups pull their units from per-XCD queues;
 * n at most the CU count: one workgroup of two 4-wave groups per row block,
   the groups taking the two halves of its KV tiles and merging in LDS (no
-  workspace).
+  workspace);
+* n at most half the CU count (one GPU's share of the heads): the same
+  two-group workgroups, but every row block split into two equal pieces on two
+  CUs that meet in a workspace.
 Checked here against the CPU oracle (same bars as the unsplit kernel: max-abs
 2e-2, mean-abs 2e-3), against the unsplit launch, run to run (bit-identical),
 with rows that see no key in one piece or in any, with garbage in the slots,
@@ -76,14 +79,30 @@ def _cus():
     return torch.cuda.get_device_properties(0).multi_processor_count
 
 
+def _uses_workspace(n):
+    """The launch of n row blocks merges pieces through the workspace: above the
+    CU count, or at most half of it."""
+    return n > _cus() or 2 * n <= _cus()
+
+
 def _n_groups(args):
     """Row blocks of one launch on this device that merge through the workspace,
-    checked against the workspace size; 0 for the two-group form (no workspace)."""
+    checked against the workspace size; 0 for the two-group form without it."""
     nmb = -(-args.SQ // 128)
-    if args.B * args.H * nmb <= _cus():
+    n = args.B * args.H * nmb
+    if not _uses_workspace(n):
         assert _ws_bytes(args) == 0
         return 0
-    ngroups, ns = _plan(args.B * args.H * nmb, nmb)
+    if n <= _cus():
+        # one two-group workgroup per CU: the plan of cus / 8 slots per XCD
+        sx = _cus() // 8
+        grid, ngroups, ns = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int32()
+        _lib.check(_lib.load().qik_attn_work_map(n, nmb, sx, 1, None, None, None, 0, ctypes.byref(grid),
+                                                 ctypes.byref(ngroups), ctypes.byref(ns)), "work map")
+        ngroups, ns = ngroups.value, ns.value
+        assert ngroups == n and ns == 2
+    else:
+        ngroups, ns = _plan(n, nmb)
     slot = 128 * args.D * 4 + 256 * 8
     assert _ws_bytes(args) == _ctl_bytes(ngroups) + ngroups * ns * slot
     return ngroups
@@ -94,6 +113,8 @@ def _workload(name):
     (432 row blocks, more than the CUs: the queue and the workspace merge)."""
     if name == "t2i_512_b2":
         return dataclasses.replace(wls.workload("t2i_512"), name=name, B=2)
+    if name.endswith("_h3"):
+        return dataclasses.replace(wls.workload(name[:-3]), name=name, H=3)
     return wls.workload(name)
 
 
@@ -119,7 +140,8 @@ def test_workspace_size_matches_the_device_plan():
     assert _n_groups(a) > 0
 
 
-@pytest.mark.parametrize("name,workspace", [("t2i_512", False), ("t2i_512_b2", True), ("multiref_cfg", True)])
+@pytest.mark.parametrize("name,workspace", [("t2i_512", False), ("t2i_512_b2", True), ("multiref_cfg", True),
+                                            ("t2i_1024_h3", True), ("edit_768_h3", True)])
 def test_split_vs_unsplit_vs_oracle(name, workspace):
     _flush(f"case split {name}")
     wl, inp = _prefill(name, seed=11)
@@ -132,7 +154,7 @@ def test_split_vs_unsplit_vs_oracle(name, workspace):
     d = (a.float() - b.float()).abs()
     # both within the oracle bar below; between them only the accumulation order differs
     assert d.max().item() <= 2 * MAX_ABS and d.mean().item() <= 5e-4, (d.max().item(), d.mean().item())
-    heads = list(range(wl.H)) if wl.B == 1 and wl.P == 0 else [3, 17]
+    heads = list(range(wl.H)) if wl.B == 1 and (wl.P == 0 or wl.H <= 4) else [3, 17]
     slab = {} if wl.P == 0 else dict(cache_k=inp["cache_k"].cpu(), cache_v=inp["cache_v"].cpu(),
                                      cache_v_scale=inp["cache_v_scale"].cpu())
     ref = oa.attention_fp32(inp["query"].cpu(), inp["key"].cpu(), inp["value"].cpu(), wl.lengths(), None,
@@ -149,7 +171,8 @@ def test_split_dtypes_and_head_dims(dtype, D, H):
     """128 text + 1024 image rows over 1152 keys: 18 KV tiles per image row block, so
     every image row block of this one-round launch is split and merged (both pieces
     non-empty), in both element types and both head dims; 4 heads (36 row blocks)
-    take the two-group form, 32 heads (288) the queue and the workspace."""
+    take two-group workgroups with every row block split over two CUs, 32 heads
+    (288) the queue; both merge through the workspace."""
     _flush(f"case split dtype={dtype} D={D} H={H}")
     g = torch.Generator().manual_seed(30 + D + H)
     S = 1152
@@ -159,7 +182,7 @@ def test_split_dtypes_and_head_dims(dtype, D, H):
     Ld = torch.from_numpy(L).to(DEV)
     out = qik.block_causal_flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), Ld, None)
     args = make_args(q.to(DEV), k.to(DEV), v.to(DEV), Ld, None, out, None, None, None, False)
-    assert (_n_groups(args) > 0) == (H * 9 > _cus())
+    assert (_n_groups(args) > 0) == _uses_workspace(H * 9)
     assert out.dtype == dtype
     _check(out, oa.attention_fp32(q, k, v, L), f"{dtype} D={D}")
     again = qik.block_causal_flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), Ld, None)
@@ -183,12 +206,12 @@ def test_split_decode_against_fp8_slab(H):
     out = qik.block_causal_flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), L, None, cache_k=kc, cache_v=vc,
                                            cache_v_scale=sc, uniform_full=True)
     args = make_args(q.to(DEV), k.to(DEV), v.to(DEV), None, None, out, kc, vc, sc, True)
-    assert (_n_groups(args) > 0) == (B * H * 5 > _cus())
+    assert (_n_groups(args) > 0) == _uses_workspace(B * H * 5)
     ref = oa.attention_fp32(q, k, v, L.cpu().numpy(), None, kc.cpu(), vc.cpu(), sc.cpu())
     _check(out, ref, "fp8 slab decode")
 
 
-@pytest.mark.parametrize("name", ["t2i_512", "t2i_512_b2"])
+@pytest.mark.parametrize("name", ["t2i_512", "t2i_512_b2", "t2i_1024_h3"])
 def test_split_is_bit_identical_run_to_run(name):
     """Whichever piece arrives last merges, in piece order: the result never changes."""
     _flush(f"case split determinism {name}")
@@ -202,7 +225,8 @@ def test_split_is_bit_identical_run_to_run(name):
 def test_rows_without_keys_in_one_piece_or_any(H):
     """1024 keys = 16 tiles, two pieces of 8: rows with L < 512 see nothing in piece 1,
     rows with L = -1 nothing at all (zeros); key_valid clears piece 0 for batch 1
-    (3 heads: the two-group form; 48 heads: the workspace merge)."""
+    (3 heads: two-group workgroups, every row block split over two CUs; 48 heads:
+    the queue and the workspace merge)."""
     _flush(f"case split empty halves H={H}")
     g = torch.Generator().manual_seed(13)
     B, SQ, SN, D = 2, 640, 1024, 128
@@ -221,7 +245,7 @@ def test_rows_without_keys_in_one_piece_or_any(H):
     a = qik.block_causal_flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), Ld, kv.to(DEV))
     b = qik.block_causal_flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), Ld, kv.to(DEV), split_tail=False)
     args = make_args(q.to(DEV), k.to(DEV), v.to(DEV), Ld, kv.to(DEV).to(torch.uint8), a, None, None, None, False)
-    assert (_n_groups(args) > 0) == (B * H * 5 > _cus())
+    assert (_n_groups(args) > 0) == _uses_workspace(B * H * 5)
     ref = oa.attention_fp32(q, k, v, L, kv.numpy())
     _check(a, ref, "split")
     _check(b, ref, "unsplit")
@@ -237,7 +261,7 @@ def _direct(inp, wl, ws, nbytes):
     return st, out, args
 
 
-@pytest.mark.parametrize("name", ["t2i_512_b2", "edit_768"])
+@pytest.mark.parametrize("name", ["t2i_512_b2", "edit_768", "edit_768_h3"])
 def test_workspace_control_words_return_to_zero(name):
     """Only the control words must start at zero: the slots may hold anything.  Every
     launch leaves the control words zero again, so the next launch reuses the buffer."""
@@ -292,7 +316,7 @@ def test_workspace_checks_are_host_side():
     torch.cuda.synchronize()
 
 
-@pytest.mark.parametrize("name", ["t2i_512", "t2i_512_b2"])
+@pytest.mark.parametrize("name", ["t2i_512", "t2i_512_b2", "edit_768_h3"])
 def test_split_under_graph_replay(name):
     """Captured once, replayed several times with eager launches (on the cached
     workspace) between replays: every replay equals the eager result."""

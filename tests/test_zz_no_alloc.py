@@ -5,8 +5,10 @@ whose control words the call clears with a fill kernel.  Checked through the
 C ABI against qik_attn_fwd_ws (same kernel and work plan, so bit-identical)
 on two calls in a row, the second with a smaller input (the array then holds
 the first call's slots), and against the CPU oracle at the attention bar.
-Launches of at most one row block per CU take the two-group form, which
-needs no workspace: there the entry point does not touch the array.
+Launches of more than half and at most one row block per CU take the
+two-group form without a workspace: there the entry point does not touch the
+array (the tiny layout, with fewer row blocks, splits them over two CUs and
+uses it).
 """
 
 import ctypes
