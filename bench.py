@@ -68,6 +68,9 @@ def parse():
     ap.add_argument("--all-workloads", action="store_true",
                     help="instead of the benchmark, time every workload of the benchmark set (t2i_512, "
                          "t2i_1024, edit_768, multiref_cfg), print one JSON line and exit")
+    ap.add_argument("--head-share", action="store_true",
+                    help="instead of the benchmark, time one GPU's share of the heads (H/n for n = 1, 2, 4, "
+                         "8) of t2i_1024 and edit_768, print one JSON line and exit")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="instead of the benchmark, run 5 plain device copies of this many MiB "
                          "(reference point for the FETCH_SIZE / WRITE_SIZE counters) and exit")
@@ -121,15 +124,12 @@ def cpu_leg(wl, inp, out, budget_s: float) -> dict:
             "heads_compared": len(heads)}
 
 
-def all_workloads(cpu_seconds: float = 3.0) -> None:
-    """Kernel time of every workload of the benchmark set through qik_attn_fwd_ws.
+def _ws_launches(wl, nl: int, seed: int, dev):
+    """``nl`` independent layers of workload ``wl`` as prebuilt qik_attn_fwd_ws launches.
 
-    Per workload: 8 independent layers launched back to back (multiref_cfg:
-    4), 3 warm-up passes, then 5 groups of 4 passes with HIP events around
-    each group; the median group gives the time per launch.  Then the CPU
-    baseline leg (``cpu_leg``) on about ``cpu_seconds`` of heads of the first
-    layer, with the GPU output of those heads compared against it.
-    """
+    Returns (layers, calls, run): the input dicts, (args, workspace, bytes,
+    output) per layer, and a function launching every layer once on the
+    current stream."""
     import ctypes
 
     import torch
@@ -139,42 +139,67 @@ def all_workloads(cpu_seconds: float = 3.0) -> None:
     from qwen_image_kernel_amd.attention import make_args
 
     lib = _lib.load()
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    layers = [wls.make_inputs(wl, seed=seed + i, device="cuda", gen_device="cuda") for i in range(nl)]
+    calls = []
+    for inp in layers:
+        out = torch.empty_like(inp["query"])
+        L = None if wl.uniform else inp["prefix_lengths"]
+        a = make_args(inp["query"], inp["key"], inp["value"], L, None, out, inp["cache_k"], inp["cache_v"],
+                      inp["cache_v_scale"], wl.uniform)
+        nb = ctypes.c_int64()
+        _lib.check(lib.qik_attn_workspace_size(ctypes.byref(a), ctypes.byref(nb)), "qik_attn_workspace_size")
+        ws = torch.zeros(max(nb.value, 256), dtype=torch.uint8, device=dev)
+        calls.append((a, ws, nb.value, out))
+
+    def run():
+        for a, ws, nb, _ in calls:
+            _lib.check(lib.qik_attn_fwd_ws(ctypes.byref(a), ws.data_ptr(), nb, stream), "qik_attn_fwd_ws")
+
+    return layers, calls, run
+
+
+def _us_per_launch(run, n_calls: int, groups: int = 5, passes: int = 4) -> float:
+    """3 warm-up passes, then ``groups`` groups of ``passes`` passes with HIP
+    events around each group; the median group's time per launch in us."""
+    import torch
+
+    for _ in range(3):
+        run()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(groups):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(passes):
+            run()
+        e1.record()
+        torch.cuda.synchronize()
+        ts.append(e0.elapsed_time(e1) * 1e3 / (passes * n_calls))
+    return sorted(ts)[len(ts) // 2]
+
+
+def all_workloads(cpu_seconds: float = 3.0) -> None:
+    """Kernel time of every workload of the benchmark set through qik_attn_fwd_ws.
+
+    Per workload: 8 independent layers launched back to back (multiref_cfg:
+    4), 3 warm-up passes, then 5 groups of 4 passes with HIP events around
+    each group; the median group gives the time per launch.  Then the CPU
+    baseline leg (``cpu_leg``) on about ``cpu_seconds`` of heads of the first
+    layer, with the GPU output of those heads compared against it.
+    """
+    import torch
+
+    import qwen_image_kernel_amd.workloads as wls
+
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     res, runs = {}, []
     for name in ("t2i_512", "t2i_1024", "edit_768", "multiref_cfg", "ref_decode_1024"):
         wl = wls.workload(name)
         nl = 4 if name == "multiref_cfg" else 8
-        layers = [wls.make_inputs(wl, seed=40 + i, device="cuda", gen_device="cuda") for i in range(nl)]
-        calls = []
-        for inp in layers:
-            out = torch.empty_like(inp["query"])
-            L = None if wl.uniform else inp["prefix_lengths"]
-            a = make_args(inp["query"], inp["key"], inp["value"], L, None, out, inp["cache_k"], inp["cache_v"],
-                          inp["cache_v_scale"], wl.uniform)
-            nb = ctypes.c_int64()
-            _lib.check(lib.qik_attn_workspace_size(ctypes.byref(a), ctypes.byref(nb)), "qik_attn_workspace_size")
-            ws = torch.zeros(max(nb.value, 256), dtype=torch.uint8, device=dev)
-            calls.append((a, ws, nb.value, out))
-
-        def run(calls=calls):
-            for a, ws, nb, _ in calls:
-                _lib.check(lib.qik_attn_fwd_ws(ctypes.byref(a), ws.data_ptr(), nb, stream), "qik_attn_fwd_ws")
-
-        for _ in range(3):
-            run()
-        torch.cuda.synchronize()
-        ts = []
-        for _ in range(5):
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
-            for _ in range(4):
-                run()
-            e1.record()
-            torch.cuda.synchronize()
-            ts.append(e0.elapsed_time(e1) * 1e3 / (4 * len(calls)))
-        us = sorted(ts)[len(ts) // 2]
+        layers, calls, run = _ws_launches(wl, nl, 40, dev)
+        us = _us_per_launch(run, len(calls))
         tf = wl.flops() / us / 1e6
         res[name] = {"us_per_launch": round(us, 2), "tflops": round(tf, 1),
                      "pct_bf16_peak": round(100 * tf / PEAK_BF16_TFLOPS, 2), "layers": nl,
@@ -187,6 +212,40 @@ def all_workloads(cpu_seconds: float = 3.0) -> None:
         if name in ("t2i_1024", "edit_768"):
             runs.append((name, run))
     print(json.dumps({"all_workloads": res, "gpu_clock": clock_under_load(runs, dev, 1.5)}), flush=True)
+
+
+def head_share() -> None:
+    """One GPU's share of the heads of the two headline shapes, through qik_attn_fwd_ws.
+
+    Attention shards by head without communication: on n GPUs each runs the
+    same sequence with H/n heads.  For n = 1, 2, 4, 8 (H = 24, 12, 6, 3) this
+    times 8 independent layers of that share launched back to back, as
+    ``all_workloads`` does, and reports the time per launch, TFLOP/s against
+    the bf16 peak, the row blocks of the launch and the workspace it takes.
+    """
+    import dataclasses
+
+    import torch
+
+    import qwen_image_kernel_amd.workloads as wls
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    res = {}
+    for name in ("t2i_1024", "edit_768"):
+        base = wls.workload(name)
+        for n in (1, 2, 4, 8):
+            wl = dataclasses.replace(base, H=base.H // n)
+            _, calls, run = _ws_launches(wl, 8, 60, dev)
+            us = _us_per_launch(run, len(calls))
+            tf = wl.flops() / us / 1e6
+            key = f"{name}_h{wl.H}"
+            res[key] = {"gpus_sharing": n, "heads": wl.H, "us_per_launch": round(us, 2),
+                        "tflops": round(tf, 1), "pct_bf16_peak": round(100 * tf / PEAK_BF16_TFLOPS, 2),
+                        "row_blocks": wl.B * wl.H * -(-wl.SQ // 128), "workspace_bytes": calls[0][2],
+                        "unmasked_gflop": round(wl.flops() / 1e9, 3)}
+            print(key, json.dumps(res[key]), file=sys.stderr, flush=True)
+    print(json.dumps({"head_share": res}), flush=True)
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "attn_fwd_traffic.txt")
@@ -585,6 +644,9 @@ def main():
         return
     if args.all_workloads:
         all_workloads(min(args.cpu_seconds, 4.0))
+        return
+    if args.head_share:
+        head_share()
         return
 
     import torch

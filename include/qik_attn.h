@@ -131,9 +131,11 @@ int qik_attn_workspace_size(const qik_attn_args* args, int64_t* bytes);
 /* qik_attn_fwd for the whole device at once: the launch holds as many
  * workgroups as the device keeps resident, and they pull row blocks (and the
  * pieces of split row blocks) from one queue per XCD, so both workgroup
- * slots of every CU stay busy to the end; a launch of at most one row block
- * per CU runs the two-group form instead (one workgroup per row block, no
- * workspace read: `workspace` may then be NULL).  Same arguments and
+ * slots of every CU stay busy to the end; a launch of more than half and at
+ * most one row block per CU runs the two-group form instead (one workgroup
+ * per row block, no workspace read: `workspace` may then be NULL), and one of
+ * at most half a row block per CU the same workgroups on the two halves of
+ * every row block's KV tiles, merged through the workspace.  Same arguments and
  * tolerance as qik_attn_fwd, bit-identical from run to run.  `workspace`:
  * device memory of the current device, 256-byte aligned, >= qik_attn_workspace_size bytes,
  * its first QIK_ATTN_WS_CTL_BYTES ZEROED ONCE before its first use (e.g.
