@@ -5,7 +5,7 @@ The host quantiser replaces ``quantize_weight_tensorwise`` (fp8.py:56-60) for a
 weight in host memory, so it must give the bytes the reference's own torch ops
 give on the CPU: scale = (amax / 448).clamp_min(1e-12) and codes =
 (w / scale).clamp(+-448).to(float8_e4m3fn), both divisions true fp32 divisions.
-Those torch ops are the checker here, plus the oracle's encoder (pinned
+Those torch ops are what the tests compare with, plus the oracle's encoder (pinned
 against torch's cast and the format's closed form in test_oracle_fp8.py).
 """
 
