@@ -584,3 +584,77 @@ def test_layers_independent_seeds_size_independent_property():
     o3 = qik.block_causal_flash_attention(q, k, vs, L, None).float()
     d = (o3 - (0.5 * o1 + 0.25 * o2)).abs()
     assert d.max().item() < 2e-2 and d.mean().item() < 2e-3
+
+
+def _random_configs(n, seed):
+    """Seeded argument sets over the whole entry point: head dims 32-256,
+    bf16 / fp16, batch 1-2, 1-5 heads, no slab or a bf16 / fp16 / fp8-V slab
+    of 1-599 keys, 1-699 fresh keys, 1-899 query rows (independent of the key
+    count), causal lengths from block-causal segments, sorted or unsorted
+    random values (some below -1 or past the last key), or uniform, an
+    optional key_valid mask in runs, and both launches."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        D = int(rng.choice([32, 64, 128, 128, 128, 256]))
+        fp16 = bool(rng.random() < 0.3)
+        cache = str(rng.choice(["none", "same", "fp8"]))
+        if fp16 and cache == "fp8":
+            cache = "same"  # the reference dequantises fp8 V to bf16 (triton_attention.py:159)
+        P = 0 if cache == "none" else int(rng.integers(1, 600))
+        lengths = str(rng.choice(["segments", "sorted", "unsorted", "uniform"]))
+        out.append(dict(seed=seed * 100 + i, D=D, fp16=fp16, B=int(rng.integers(1, 3)), H=int(rng.integers(1, 6)),
+                        cache=cache, P=P, SN=int(rng.integers(1, 700)), SQ=int(rng.integers(1, 900)),
+                        lengths=lengths, key_valid=bool(rng.random() < 0.35) and lengths != "uniform",
+                        split=bool(rng.random() < 0.7)))
+    return out
+
+
+@pytest.mark.parametrize("cfg", _random_configs(64, 31), ids=lambda c: f"s{c['seed']}")
+def test_random_configurations_vs_oracle(cfg):
+    """Each seeded argument set through block_causal_flash_attention against
+    the fp32 explicit-mask oracle at the usual bar."""
+    _flush(f"case random {cfg}")
+    rng = np.random.default_rng(cfg["seed"])
+    g = torch.Generator().manual_seed(cfg["seed"])
+    dtype = torch.float16 if cfg["fp16"] else torch.bfloat16
+    B, H, D, P, SN, SQ = cfg["B"], cfg["H"], cfg["D"], cfg["P"], cfg["SN"], cfg["SQ"]
+    KV = P + SN
+    q = _rand((B, SQ, H, D), g, 1.0, dtype)
+    kn, vn = (_rand((B, SN, H, D), g, 1.0, dtype) for _ in range(2))
+    ck = cv = sc = None
+    if P > 0:
+        kp, vp = (_rand((B, P, H, D), g, 1.0, dtype) for _ in range(2))
+        cache = qik.ContiguousKVCache(1, B, P + int(rng.integers(0, 100)), H, D, dtype=dtype,
+                                      v_fp8=cfg["cache"] == "fp8", device=DEV)
+        cache.get_layer(0).store(kp.to(DEV), vp.to(DEV))
+        ck, cv, sc = cache.get_layer(0).views()
+    if cfg["lengths"] == "segments":
+        layout, left = [], SQ
+        while left > 0:
+            n = int(min(left, rng.integers(1, 300)))
+            layout.append((str(rng.choice(["text", "img"])), n))
+            left -= n
+        segs, S0 = ol.make_segments(layout)
+        L = (ol.build_prefix_lengths(segs, S0, SQ) + P).clip(max=KV - 1).astype(np.int32)
+    elif cfg["lengths"] == "uniform":
+        L = np.full(SQ, KV - 1, dtype=np.int32)
+    else:
+        L = rng.integers(-3, KV + 40, size=SQ).astype(np.int32)
+        if cfg["lengths"] == "sorted":
+            L = np.sort(L)
+    kv = None
+    if cfg["key_valid"]:
+        kv = torch.ones(B, KV, dtype=torch.bool)
+        for _ in range(int(rng.integers(1, 6))):
+            b0, s0 = int(rng.integers(0, B)), int(rng.integers(0, KV))
+            kv[b0, s0:s0 + int(rng.integers(1, 90))] = False
+    out = qik.block_causal_flash_attention(
+        q.to(DEV), kn.to(DEV), vn.to(DEV), torch.from_numpy(L).to(DEV), None if kv is None else kv.to(DEV),
+        cache_k=ck, cache_v=cv, cache_v_scale=sc if cfg["cache"] == "fp8" else None,
+        uniform_full=cfg["lengths"] == "uniform", split_tail=cfg["split"])
+    torch.cuda.synchronize()
+    assert out.dtype == dtype and out.shape == q.shape
+    ref = oa.attention_fp32(q, kn, vn, L, kv, None if ck is None else ck.cpu(), None if cv is None else cv.cpu(),
+                            sc.cpu() if cfg["cache"] == "fp8" else None)
+    _check(out, ref, what=f"random {cfg['seed']}")
