@@ -36,6 +36,11 @@
 //   * Row blocks reach workgroups through per-XCD queues (qik_plan.h): one
 //     (b, h)'s row blocks share an XCD and its L2, heaviest first, and with a
 //     workspace the last partial round runs as two pieces per row block.
+//   * A launch of at most one row block per CU runs the two-group kernel
+//     (KSPLIT = 2): 8-wave workgroups whose two 4-wave groups split a row
+//     block's KV tiles and merge in LDS; with at most half a row block per CU,
+//     every row block is also cut in two pieces on two CUs, merged through the
+//     workspace.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
