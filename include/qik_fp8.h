@@ -122,6 +122,17 @@ int qik_fp8_gemm(const qik_fp8_gemm_args* args, void* stream);
 int qik_fp8_gemm_workspace_size(const qik_fp8_gemm_args* args, int64_t* bytes);
 int qik_fp8_gemm_ws(const qik_fp8_gemm_args* args, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* The launch qik_fp8_gemm_ws makes for an M x N x K product on a device with
+ * `cus` compute units (0: 256), host only, no device involved (no counterpart
+ * in the reference; for tests and tooling, as qik_attn_work_map is for the
+ * attention launch).  plan[0..5] = big tile rows, big tile columns, small
+ * tile rows, small tile columns, 1 when the small tiles' workgroups come
+ * first in blockIdx order, the number of K slices (1: no split); *n1 = the
+ * output columns [0, n1) the big tiles cover (N for a K split, which runs
+ * 128 x 128 tiles only).  QIK_ERR_SHAPE for a shape qik_fp8_gemm_validate
+ * refuses (with its strides equal to K, K and N). */
+int qik_fp8_gemm_plan(int64_t M, int64_t N, int64_t K, int32_t cus, int32_t* plan, int64_t* n1);
+
 /* out[i] = round(fp32(code[i]) * scale[0]) into out_dtype, for i < n: the
  * dequantised weight of the bf16 path (fp8.py:81: fp8 -> bf16 -> fp32 is
  * exact, one fp32 multiply).  out_dtype QIK_DTYPE_BF16 or QIK_DTYPE_FP16

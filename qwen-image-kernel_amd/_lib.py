@@ -235,6 +235,9 @@ EXPORTS = (
      (ctypes.POINTER(QikFp8GemmArgs), ctypes.POINTER(ctypes.c_int64))),
     ("qik_fp8_gemm_ws", ctypes.c_int,
      (ctypes.POINTER(QikFp8GemmArgs), ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p)),
+    ("qik_fp8_gemm_plan", ctypes.c_int,
+     (ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, ctypes.POINTER(ctypes.c_int32),
+      ctypes.POINTER(ctypes.c_int64))),
     ("qik_fp8_dequant", ctypes.c_int,
      (ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p)),
     ("qik_fp8_quantize_weight_host", ctypes.c_int,

@@ -1646,6 +1646,28 @@ int qik_fp8_gemm_ws(const qik_fp8_gemm_args* a, void* workspace, int64_t workspa
   return hipLaunchKernel(fr, dim3((unsigned)rgrid), dim3(256), args, 0, s) == hipSuccess ? QIK_OK : QIK_ERR_LAUNCH;
 }
 
+int qik_fp8_gemm_plan(int64_t M, int64_t N, int64_t K, int32_t cus, int32_t* plan, int64_t* n1) {
+  using namespace qik_fp8;
+  if (plan == nullptr || n1 == nullptr) return QIK_ERR_NULL_ARG;
+  if (M < 1 || N < 16 || K < 16 || N % 16 != 0 || K % 16 != 0) return QIK_ERR_SHAPE;
+  if (M > (int64_t)INT_MAX || N > (int64_t)INT_MAX || K > (int64_t)(INT_MAX / 256)) return QIK_ERR_SHAPE;
+  if (cus <= 0) cus = 256;
+  const int S = choose_ksplit(M, N, K, cus);
+  if (S > 1) {
+    const int32_t v[6] = {128, 128, 128, 128, 0, S};
+    memcpy(plan, v, sizeof(v));
+    *n1 = N;
+    return QIK_OK;
+  }
+  const GemmPlan g = choose_plan(M, N, cus);
+  const TileShape& s1 = kShapes[kPairs[g.pair][0]];
+  const TileShape& s2 = kShapes[kPairs[g.pair][1]];
+  const int32_t v[6] = {s1.bm, s1.bn, s2.bm, s2.bn, g.small_first ? 1 : 0, 1};
+  memcpy(plan, v, sizeof(v));
+  *n1 = g.n1;
+  return QIK_OK;
+}
+
 int qik_fp8_dequant(const void* w, const float* scale, void* out, int64_t n, int32_t out_dtype, void* stream) {
   using namespace qik_fp8;
   if (out_dtype != QIK_DTYPE_BF16 && out_dtype != QIK_DTYPE_FP16 && out_dtype != QIK_DTYPE_FP32)

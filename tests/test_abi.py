@@ -382,6 +382,36 @@ def test_fp8_gemm_workspace_size_and_checks():
     assert lib.qik_fp8_gemm_ws(ctypes.byref(_gemm_args(M=0)), base, n.value, None) == -5
 
 
+@pytest.mark.parametrize("mnk,plan,n1", [
+    ((1536, 4096, 4096), [192, 128, 128, 128, 0, 1], 4096),    # 256 tiles of 192 x 128, one per CU
+    ((4352, 9216, 3072), [256, 256, 256, 128, 1, 1], 7680),    # fused QKV: 256 x 128 columns launched first
+    ((4352, 12288, 3072), [256, 256, 256, 128, 1, 1], 11520),  # MLP in: the same
+    ((4352, 3072, 12288), [256, 256, 256, 128, 0, 1], 3072),   # MLP out: 204 tiles of 256 x 256
+    ((256, 9216, 3072), [256, 128, 128, 128, 0, 1], 0),        # text QKV: 144 tiles of 128 x 128
+    ((256, 3072, 12288), [128, 128, 128, 128, 0, 5], 3072),    # text MLP out: K split in 5
+    ((1543, 9232, 1104), [256, 256, 256, 128, 0, 1], 8192),    # small tiles first would finish later
+    ((100, 1040, 8192), [128, 128, 128, 128, 0, 8], 1040),     # K split in 8
+])
+def test_fp8_gemm_plan(mnk, plan, n1):
+    """The host mirror of the GEMM launch (256 CUs, the count the host assumes
+    without a device): tile shapes, the columns of the big tiles, which region
+    goes first, the K split."""
+    lib = _lib.load()
+    got = (ctypes.c_int32 * 6)()
+    n = ctypes.c_int64()
+    assert lib.qik_fp8_gemm_plan(*mnk, 0, got, ctypes.byref(n)) == 0
+    assert list(got) == plan and n.value == n1
+
+
+def test_fp8_gemm_plan_checks():
+    lib = _lib.load()
+    got = (ctypes.c_int32 * 6)()
+    n = ctypes.c_int64()
+    assert lib.qik_fp8_gemm_plan(0, 16, 16, 0, got, ctypes.byref(n)) == -5
+    assert lib.qik_fp8_gemm_plan(16, 24, 16, 0, got, ctypes.byref(n)) == -5
+    assert lib.qik_fp8_gemm_plan(16, 16, 16, 0, None, None) == -1
+
+
 def _quant_args(**kw):
     a = _lib.QikFp8QuantArgs()
     a.abi_version = _lib.ABI_VERSION
